@@ -1,0 +1,132 @@
+"""ctypes binding of libbzgemv.so (the C ABI declared in include/bz_gemv.h).
+
+torch is imported before the library is opened: both link the HIP runtime by
+its SONAME (libamdhip64.so.7), so the library binds to the runtime torch has
+already loaded and the hipStream_t / device pointers torch hands out are valid
+in it.  There is no fallback: if the library is missing the import fails.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede loading the HIP library)
+
+LIB_PATH = Path(os.environ.get("BZ_LIB", str(Path(__file__).resolve().parent / "libbzgemv.so")))
+ABI_VERSION = 1
+
+# enums of include/bz_gemv.h
+OK = 0
+ERR_INVALID_ARG, ERR_SHAPE, ERR_ALIGNMENT, ERR_UNSUPPORTED, ERR_LAUNCH, ERR_ABI = 1, 2, 3, 4, 5, 6
+W_INT4_ZP, W_INT4_MIN, W_FP8, W_BF16 = 0, 1, 2, 3
+EPI_NONE, EPI_SILU_GATE, EPI_RESIDUAL = 0, 1, 2
+DT_BF16, DT_F32 = 0, 1
+
+EXPORTS = (
+    "bz_abi_version",
+    "bz_strerror",
+    "bz_gemv_workspace",
+    "bz_gemv",
+    "bz_rmsnorm",
+    "bz_silu_mul",
+    "bz_quantize_int4",
+    "bz_quantize_fp8",
+    "bz_dequant",
+)
+
+
+class GemvDesc(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("M", ctypes.c_int32),
+        ("N", ctypes.c_int32),
+        ("K", ctypes.c_int32),
+        ("group", ctypes.c_int32),
+        ("wfmt", ctypes.c_int32),
+        ("epilogue", ctypes.c_int32),
+        ("out_dtype", ctypes.c_int32),
+        ("residual_dtype", ctypes.c_int32),
+        ("cfg_nch", ctypes.c_int32),
+        ("cfg_nw", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+        ("x", ctypes.c_void_p),
+        ("ldx", ctypes.c_int64),
+        ("w", ctypes.c_void_p),
+        ("sc0", ctypes.c_void_p),
+        ("sc1", ctypes.c_void_p),
+        ("gamma", ctypes.c_void_p),
+        ("residual", ctypes.c_void_p),
+        ("ldr", ctypes.c_int64),
+        ("out", ctypes.c_void_p),
+        ("ldo", ctypes.c_int64),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+class BzError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        self.status = status
+        super().__init__(f"{what}: {strerror(status)} (status {status})")
+
+
+_lib: ctypes.CDLL | None = None
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    vp, i32, i64, f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
+    lib.bz_abi_version.restype = ctypes.c_int
+    lib.bz_abi_version.argtypes = []
+    lib.bz_strerror.restype = ctypes.c_char_p
+    lib.bz_strerror.argtypes = [ctypes.c_int]
+    lib.bz_gemv_workspace.restype = ctypes.c_size_t
+    lib.bz_gemv_workspace.argtypes = [ctypes.POINTER(GemvDesc)]
+    lib.bz_gemv.restype = ctypes.c_int
+    lib.bz_gemv.argtypes = [ctypes.POINTER(GemvDesc), vp]
+    lib.bz_rmsnorm.restype = ctypes.c_int
+    lib.bz_rmsnorm.argtypes = [vp, i64, vp, f32, vp, i64, i32, i32, vp]
+    lib.bz_silu_mul.restype = ctypes.c_int
+    lib.bz_silu_mul.argtypes = [vp, i64, vp, i64, vp, i64, i32, i32, vp]
+    lib.bz_quantize_int4.restype = ctypes.c_int
+    lib.bz_quantize_int4.argtypes = [vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp]
+    lib.bz_quantize_fp8.restype = ctypes.c_int
+    lib.bz_quantize_fp8.argtypes = [vp, i32, i32, i32, f32, vp, vp, vp]
+    lib.bz_dequant.restype = ctypes.c_int
+    lib.bz_dequant.argtypes = [i32, vp, vp, vp, i32, i32, i32, vp, vp]
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m breeze_amd.build` "
+                "(the GPU path has no fallback)"
+            )
+        handle = ctypes.CDLL(str(LIB_PATH), mode=ctypes.RTLD_GLOBAL)
+        _declare(handle)
+        version = handle.bz_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI {version}, this binding expects {ABI_VERSION}")
+        _lib = handle
+    return _lib
+
+
+def strerror(status: int) -> str:
+    try:
+        return lib().bz_strerror(status).decode()
+    except Exception:  # noqa: BLE001 - only used to format an error
+        return "unknown"
+
+
+def check(status: int, what: str) -> None:
+    if status != OK:
+        raise BzError(status, what)
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """Raw hipStream_t of torch's current stream on t's device."""
+    return torch.cuda.current_stream(t.device).cuda_stream

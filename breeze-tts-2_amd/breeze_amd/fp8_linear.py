@@ -1,0 +1,104 @@
+"""FP8 (OCP e4m3) weight Linear for bandwidth-bound decode, on MI355X.
+
+Drop-in for models/fp8_linear.py: same names (FP8_MAX, FP8_DTYPE,
+MIN_QUANT_BYTES, DEFAULT_TARGET_NAMES, Fp8Linear, quantize_module_fp8), same
+buffers (``weight_fp8`` float8_e4m3fn [N, K], ``weight_scale`` fp32 (1, N))
+computed by the same formula (models/fp8_linear.py:58-66), same stats dict.
+
+forward() is the weight-only form: bf16 activations times e4m3 weights with
+fp32 accumulation and the per-channel scale applied to the dot product, i.e.
+exactly ``x @ (w8.float() * s).T`` of the reference's own correctness
+definition (bench_gemv.py:49) and its fused path
+(models/fused/kernels.py:84-85,124-126).  The reference's
+``Fp8Linear.forward`` additionally rounds the activations to fp8 per row
+before ``_scaled_mm`` (models/fp8_linear.py:72-82); that extra rounding is
+not reproduced (it only adds error), since decode here is bound by the weight
+bytes, not by the arithmetic.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from .gemv import W_FP8, gemv_traceable, quantize_fp8_device
+
+# Max representable magnitude of float8_e4m3fn.
+FP8_MAX = 448.0
+FP8_DTYPE = torch.float8_e4m3fn
+
+MIN_QUANT_BYTES = 8 * 1024 * 1024
+
+DEFAULT_TARGET_NAMES = ("gate_proj", "up_proj", "down_proj")
+
+# amax floor of Fp8Linear (models/fp8_linear.py:58)
+AMAX_FLOOR = 1e-12
+
+
+class Fp8Linear(nn.Module):
+    """Drop-in replacement for a bias-free nn.Linear using FP8 weights."""
+
+    def __init__(self, linear: nn.Linear) -> None:
+        super().__init__()
+        if linear.bias is not None:
+            raise ValueError("Fp8Linear expects a bias-free Linear")
+
+        weight = linear.weight.data
+        self.in_features = int(weight.shape[1])
+        self.out_features = int(weight.shape[0])
+        if self.in_features % 16:
+            raise ValueError(f"in_features {self.in_features} must be a multiple of 16 for the fp8 GEMV")
+
+        codes, scale = quantize_fp8_device(weight, AMAX_FLOOR)
+        if weight.device.type != "cuda":
+            codes, scale = codes.to(weight.device), scale.to(weight.device)
+        self.register_buffer("weight_fp8", codes.contiguous())
+        self.register_buffer("weight_scale", scale.reshape(1, -1).contiguous())
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        shape = x.shape
+        flat = x.reshape(-1, shape[-1])
+        out = gemv_traceable(
+            flat.to(torch.bfloat16),
+            self.weight_fp8.view(torch.uint8),
+            W_FP8,
+            self.out_features,
+            sc0=self.weight_scale,
+        )
+        return out.to(x.dtype).reshape(*shape[:-1], self.out_features)
+
+    def extra_repr(self) -> str:
+        return f"in_features={self.in_features}, out_features={self.out_features}, fp8=True"
+
+
+def quantize_module_fp8(
+    root: nn.Module,
+    *,
+    target_names: tuple[str, ...] = DEFAULT_TARGET_NAMES,
+    min_bytes: int = MIN_QUANT_BYTES,
+) -> dict[str, int]:
+    """Swap qualifying Linear layers under ``root`` for FP8 equivalents
+    (models/fp8_linear.py:89-122)."""
+    converted = 0
+    saved_bytes = 0
+    skipped_small = 0
+
+    for module in root.modules():
+        for child_name, child in list(module.named_children()):
+            if not isinstance(child, nn.Linear) or child.bias is not None:
+                continue
+            if target_names and child_name not in target_names:
+                continue
+            nbytes = child.weight.numel() * child.weight.element_size()
+            if nbytes < min_bytes:
+                skipped_small += 1
+                continue
+            setattr(module, child_name, Fp8Linear(child))
+            converted += 1
+            saved_bytes += nbytes // 2
+
+    return {
+        "converted": converted,
+        "skipped_below_threshold": skipped_small,
+        "weight_bytes_saved": saved_bytes,
+    }

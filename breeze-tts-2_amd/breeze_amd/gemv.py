@@ -1,0 +1,298 @@
+"""torch-facing wrappers of the C ABI (include/bz_gemv.h).
+
+Every function here only checks arguments, allocates outputs with torch and
+hands raw device pointers plus torch's current HIP stream to libbzgemv.so.
+There is no CPU path: tensors must live on a GPU and the library must be
+built, otherwise the call raises.
+
+``gemv`` is also registered as the custom op ``breeze_amd::gemv`` with a
+shape-only fake implementation, so modules calling it stay traceable by
+``torch.compile(fullgraph=True)`` (the reference compiles depth layers that
+way, models/cudagraph/depth_decoder_graph.py:164-192) and capturable in HIP
+graphs (no allocation, sync or tuning inside the library call).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import (
+    DT_BF16,
+    DT_F32,
+    EPI_NONE,
+    EPI_RESIDUAL,
+    EPI_SILU_GATE,
+    W_BF16,
+    W_FP8,
+    W_INT4_MIN,
+    W_INT4_ZP,
+)
+
+__all__ = [
+    "gemv",
+    "rmsnorm",
+    "silu_mul",
+    "quantize_int4_device",
+    "quantize_fp8_device",
+    "dequant",
+    "EPI_NONE",
+    "EPI_SILU_GATE",
+    "EPI_RESIDUAL",
+    "W_INT4_ZP",
+    "W_INT4_MIN",
+    "W_FP8",
+    "W_BF16",
+]
+
+_DT = {torch.bfloat16: DT_BF16, torch.float32: DT_F32}
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _require_gpu(name: str, t: torch.Tensor, device: torch.device) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{name} must be a GPU tensor (got {t.device}); the HIP path has no CPU fallback")
+    if t.device != device:
+        raise RuntimeError(f"{name} is on {t.device}, expected {device}")
+
+
+def _rows_aligned(x: torch.Tensor) -> torch.Tensor:
+    """bf16 [M,K] view whose rows start on 16-byte boundaries (copy if not)."""
+    if x.dtype != torch.bfloat16:
+        x = x.to(torch.bfloat16)
+    if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+        if x.data_ptr() % 16:
+            x = x.clone()
+    return x
+
+
+def gemv(
+    x: torch.Tensor,
+    w: torch.Tensor,
+    wfmt: int,
+    n: int,
+    *,
+    sc0: Optional[torch.Tensor] = None,
+    sc1: Optional[torch.Tensor] = None,
+    group: int = 128,
+    gamma: Optional[torch.Tensor] = None,
+    eps: float = 1e-6,
+    epilogue: int = EPI_NONE,
+    residual: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+    out_dtype: torch.dtype = torch.bfloat16,
+    cfg: tuple[int, int] = (0, 0),
+) -> torch.Tensor:
+    """out[M, N_out] = epilogue(rmsnorm?(x) @ w_eff^T) in one launch.
+
+    x [M, K] (any float dtype; computed as bf16), weight of format ``wfmt``
+    with ``n`` rows, optional RMSNorm gamma [K], epilogue NONE / SILU_GATE
+    (N_out = n/2) / RESIDUAL (residual [M, N_out]).  Returns ``out``.
+    """
+    if x.dim() != 2:
+        raise ValueError(f"x must be 2-D [M, K], got {tuple(x.shape)}")
+    dev = x.device
+    _require_gpu("x", x, dev)
+    _require_gpu("w", w, dev)
+    M, K = x.shape
+    n_out = n // 2 if epilogue == EPI_SILU_GATE else n
+    x = _rows_aligned(x)
+    if gamma is not None:
+        _require_gpu("gamma", gamma, dev)
+        gamma = gamma.to(torch.bfloat16).contiguous()
+        if gamma.numel() != K:
+            raise ValueError(f"gamma has {gamma.numel()} elements, K = {K}")
+    res_dt = DT_BF16
+    if epilogue == EPI_RESIDUAL:
+        if residual is None:
+            raise ValueError("residual epilogue needs a residual tensor")
+        _require_gpu("residual", residual, dev)
+        if residual.dtype not in _DT:
+            residual = residual.to(out.dtype if out is not None else out_dtype)
+        if residual.shape != (M, n_out):
+            raise ValueError(f"residual shape {tuple(residual.shape)} != {(M, n_out)}")
+        if residual.stride(1) != 1:
+            residual = residual.contiguous()
+        res_dt = _DT[residual.dtype]
+    if out is None:
+        out = torch.empty(M, n_out, device=dev, dtype=out_dtype)
+    else:
+        _require_gpu("out", out, dev)
+        if out.dtype not in _DT or out.shape != (M, n_out) or out.stride(1) != 1:
+            raise ValueError("out must be a bf16/fp32 [M, N_out] row-major tensor")
+    for name, t in (("sc0", sc0), ("sc1", sc1)):
+        if t is not None:
+            _require_gpu(name, t, dev)
+    d = _lib.GemvDesc()
+    d.abi_version = _lib.ABI_VERSION
+    d.M, d.N, d.K = M, n, K
+    d.group = group
+    d.wfmt = wfmt
+    d.epilogue = epilogue
+    d.out_dtype = _DT[out.dtype]
+    d.residual_dtype = res_dt
+    d.cfg_nch, d.cfg_nw = cfg
+    d.eps = eps
+    d.x, d.ldx = x.data_ptr(), x.stride(0)
+    d.w = w.data_ptr()
+    d.sc0 = _ptr(sc0)
+    d.sc1 = _ptr(sc1)
+    d.gamma = _ptr(gamma)
+    if epilogue == EPI_RESIDUAL:
+        d.residual, d.ldr = residual.data_ptr(), residual.stride(0)
+    d.out, d.ldo = out.data_ptr(), out.stride(0)
+    _lib.check(_lib.lib().bz_gemv(ctypes.byref(d), _lib.stream_of(x)), "bz_gemv")
+    return out
+
+
+# ---- custom-op registration (torch.compile / fake tensors) -----------------
+
+
+@torch.library.custom_op("breeze_amd::gemv", mutates_args=())
+def gemv_op(
+    x: torch.Tensor,
+    w: torch.Tensor,
+    sc0: Optional[torch.Tensor],
+    sc1: Optional[torch.Tensor],
+    gamma: Optional[torch.Tensor],
+    residual: Optional[torch.Tensor],
+    wfmt: int,
+    n: int,
+    group: int,
+    eps: float,
+    epilogue: int,
+    out_f32: bool,
+) -> torch.Tensor:
+    return gemv(
+        x, w, wfmt, n, sc0=sc0, sc1=sc1, group=group, gamma=gamma, eps=eps, epilogue=epilogue,
+        residual=residual, out_dtype=torch.float32 if out_f32 else torch.bfloat16,
+    )
+
+
+@gemv_op.register_fake
+def _gemv_fake(x, w, sc0, sc1, gamma, residual, wfmt, n, group, eps, epilogue, out_f32):
+    n_out = n // 2 if epilogue == EPI_SILU_GATE else n
+    return x.new_empty((x.shape[0], n_out), dtype=torch.float32 if out_f32 else torch.bfloat16)
+
+
+def gemv_traceable(x, w, wfmt, n, *, sc0=None, sc1=None, group=128, gamma=None, eps=1e-6,
+                   epilogue=EPI_NONE, residual=None, out_dtype=torch.bfloat16):
+    """``gemv`` through the registered custom op while torch.compile traces,
+    the direct (cheaper) ctypes call otherwise."""
+    if torch.compiler.is_compiling():
+        return torch.ops.breeze_amd.gemv(
+            x, w, sc0, sc1, gamma, residual, wfmt, n, group, eps, epilogue, out_dtype == torch.float32
+        )
+    return gemv(x, w, wfmt, n, sc0=sc0, sc1=sc1, group=group, gamma=gamma, eps=eps,
+                epilogue=epilogue, residual=residual, out_dtype=out_dtype)
+
+
+# ---- glue kernels ------------------------------------------------------------
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """bf16(x * rsqrt(mean(x^2)+eps) * w) per row (models/fused/kernels.py:552-557)."""
+    _require_gpu("x", x, x.device)
+    x = x.to(torch.bfloat16)
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    M, K = x.shape
+    w = w.to(torch.bfloat16).contiguous()
+    if out is None:
+        out = torch.empty(M, K, device=x.device, dtype=torch.bfloat16)
+    _lib.check(
+        _lib.lib().bz_rmsnorm(x.data_ptr(), x.stride(0), w.data_ptr(), eps, out.data_ptr(), out.stride(0), M, K,
+                              _lib.stream_of(x)),
+        "bz_rmsnorm",
+    )
+    return out
+
+
+def silu_mul(g: torch.Tensor, u: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """silu(g) * u, bf16 (models/fused/kernels.py:570-575)."""
+    _require_gpu("g", g, g.device)
+    g = g.to(torch.bfloat16)
+    u = u.to(torch.bfloat16)
+    if g.stride(1) != 1:
+        g = g.contiguous()
+    if u.stride(1) != 1:
+        u = u.contiguous()
+    M, N = g.shape
+    if out is None:
+        out = torch.empty(M, N, device=g.device, dtype=torch.bfloat16)
+    _lib.check(
+        _lib.lib().bz_silu_mul(g.data_ptr(), g.stride(0), u.data_ptr(), u.stride(0), out.data_ptr(), out.stride(0),
+                               M, N, _lib.stream_of(g)),
+        "bz_silu_mul",
+    )
+    return out
+
+
+# ---- load-time quantizers ----------------------------------------------------
+
+
+def _weight_on_gpu(weight: torch.Tensor) -> torch.Tensor:
+    if weight.device.type != "cuda":
+        if not torch.cuda.is_available():
+            raise RuntimeError("quantization runs on the GPU (HIP kernel); no GPU is visible")
+        weight = weight.to(torch.device("cuda", torch.cuda.current_device()))
+    if weight.dtype not in (torch.float32, torch.bfloat16):
+        weight = weight.float()
+    return weight.contiguous()
+
+
+def quantize_int4_device(weight: torch.Tensor, group: int, symmetric: bool = False, layout: int = W_INT4_ZP):
+    """HIP group quantizer.  Returns (packed uint8 [N, K/2], sc0, sc1) on the
+    GPU: layout W_INT4_ZP -> sc0 = scales_zeros bf16 [K/g, N, 2], sc1 None;
+    W_INT4_MIN -> sc0 = scale bf16 [N, K/g], sc1 = min bf16 [N, K/g]."""
+    w = _weight_on_gpu(weight)
+    N, K = w.shape
+    if group < 2 or K % group:
+        raise ValueError(f"in_features {K} not divisible by group {group}")
+    G = K // group
+    packed = torch.empty(N, K // 2, device=w.device, dtype=torch.uint8)
+    if layout == W_INT4_ZP:
+        sc0 = torch.empty(G, N, 2, device=w.device, dtype=torch.bfloat16)
+        sc1 = None
+    else:
+        sc0 = torch.empty(N, G, device=w.device, dtype=torch.bfloat16)
+        sc1 = torch.empty(N, G, device=w.device, dtype=torch.bfloat16)
+    _lib.check(
+        _lib.lib().bz_quantize_int4(w.data_ptr(), _DT[w.dtype], N, K, group, int(symmetric), layout,
+                                    packed.data_ptr(), sc0.data_ptr(), _ptr(sc1), _lib.stream_of(w)),
+        "bz_quantize_int4",
+    )
+    return packed, sc0, sc1
+
+
+def quantize_fp8_device(weight: torch.Tensor, amax_floor: float):
+    """HIP per-row fp8 quantizer.  Returns (codes float8_e4m3fn [N,K], scale f32 [N])."""
+    w = _weight_on_gpu(weight)
+    N, K = w.shape
+    codes = torch.empty(N, K, device=w.device, dtype=torch.uint8)
+    scale = torch.empty(N, device=w.device, dtype=torch.float32)
+    _lib.check(
+        _lib.lib().bz_quantize_fp8(w.data_ptr(), _DT[w.dtype], N, K, amax_floor, codes.data_ptr(), scale.data_ptr(),
+                                   _lib.stream_of(w)),
+        "bz_quantize_fp8",
+    )
+    return codes.view(torch.float8_e4m3fn), scale
+
+
+def dequant(wfmt: int, w: torch.Tensor, n: int, k: int, *, sc0=None, sc1=None, group: int = 128) -> torch.Tensor:
+    """w_eff float32 [n, k] decoded by the GPU path's own unpacking code."""
+    _require_gpu("w", w, w.device)
+    out = torch.empty(n, k, device=w.device, dtype=torch.float32)
+    _lib.check(
+        _lib.lib().bz_dequant(wfmt, w.data_ptr(), _ptr(sc0), _ptr(sc1), n, k, group, out.data_ptr(),
+                              _lib.stream_of(w)),
+        "bz_dequant",
+    )
+    return out

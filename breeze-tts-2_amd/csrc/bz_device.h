@@ -1,0 +1,95 @@
+// Device helpers shared by the gfx950 kernels of libbzgemv.
+//
+// Number formats
+//   bf16   raw uint16 bit patterns; widening is a 16-bit shift, narrowing
+//          uses the hardware RNE conversion (v_cvt_pk_bf16_f32 on gfx950).
+//   int4   two nibbles per byte, even k in the low nibble.  A dword holds
+//          eight consecutive k: nibble p (bits 4p..4p+3) is k = 8d + p.
+//   e4m3   OCP FP8 E4M3 codes (no infinities, max 448), decoded by the
+//          gfx950 conversion instruction v_cvt_scalef32_pk_bf16_fp8.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bz {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+__device__ __forceinline__ bf16x2_t as_bf16x2(uint32_t v) { return __builtin_bit_cast(bf16x2_t, v); }
+
+// fp32 += a.lo*b.lo + a.hi*b.hi  (v_dot2c_f32_bf16)
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(a), as_bf16x2(b), c, false);
+}
+
+// Two nibbles -> two bf16 values 128+q.  Selects nibble p = sel (low half)
+// and p = sel+4 (high half) of `v` after the caller's shift: the bf16 with
+// exponent 2^7 and the nibble as the low mantissa bits is exactly 128 + q.
+__device__ __forceinline__ uint32_t nib2_bf16(uint32_t v) {
+    return (v & 0x000F000Fu) | 0x43004300u;
+}
+
+// Two e4m3 codes (bytes 0,1 or 2,3 of v) -> two bf16 (exact: every e4m3
+// value is a bf16 value).
+template <bool HI>
+__device__ __forceinline__ uint32_t fp8x2_bf16(uint32_t v) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v, 1.0f, HI));
+}
+
+// DPP cross-lane moves.  update_dpp(old, src, ctrl, row_mask, bank_mask, bound_ctrl).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;          // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;          // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;   // lane i <- lane 7-i inside each 8-lane half row
+
+// Sum over each aligned group of 8 lanes; every lane of the group gets it.
+__device__ __forceinline__ float sum8(float v) {
+    v += dpp_f32<kDppXor1>(v);
+    v += dpp_f32<kDppXor2>(v);
+    v += dpp_f32<kDppHalfMirror>(v);
+    return v;
+}
+
+// Sum over each aligned quad of lanes.
+__device__ __forceinline__ float sum4(float v) {
+    v += dpp_f32<kDppXor1>(v);
+    v += dpp_f32<kDppXor2>(v);
+    return v;
+}
+
+// Full-wave (64 lanes) sum, every lane gets it.  Prologue use only.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = sum8(v);
+    v += __shfl_xor(v, 8, 64);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+}  // namespace bz

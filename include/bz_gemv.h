@@ -1,0 +1,173 @@
+/*
+ * bz_gemv.h -- C ABI of libbzgemv.so, the MI355X (gfx950) decode-time linear
+ * layers of Breeze TTS 2: RMSNorm-prologue GEMV over int4 group-quantized,
+ * fp8 e4m3 (OCP) per-row-scaled or bf16 weights, with a SiLU-gate or residual
+ * epilogue, plus the load-time quantizers and two small glue kernels.
+ *
+ * Conventions
+ *   - Every pointer argument is a device pointer owned by the caller, except
+ *     the descriptor itself (host memory, read during the call only).
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *   - No call allocates memory, synchronizes the host or tunes anything, so
+ *     every call can be recorded into a HIP graph.  Calls on different
+ *     streams are independent: no call keeps global mutable device state.
+ *   - Return value: BZ_OK (0) or a bz_status error code; bz_strerror() names
+ *     it.  Errors are detected on the host before anything is launched.
+ *   - bfloat16 tensors are raw uint16 bit patterns; "bf16" below.
+ */
+#ifndef BZ_GEMV_H
+#define BZ_GEMV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BZ_ABI_VERSION 1
+
+typedef enum bz_status {
+    BZ_OK = 0,
+    BZ_ERR_INVALID_ARG = 1,  /* null pointer, bad enum, non-positive size  */
+    BZ_ERR_SHAPE = 2,        /* K not divisible by the group / format step */
+    BZ_ERR_ALIGNMENT = 3,    /* pointer or leading dimension misaligned    */
+    BZ_ERR_UNSUPPORTED = 4,  /* a valid request this build cannot run      */
+    BZ_ERR_LAUNCH = 5,       /* the HIP runtime rejected a launch          */
+    BZ_ERR_ABI = 6           /* descriptor abi_version mismatch            */
+} bz_status;
+
+/* Weight formats.  All weights are row-major over the N output channels.
+ *
+ * BZ_W_INT4_ZP : w uint8 [N][K/2]; byte j of row n holds k = 2j in the low
+ *                nibble and k = 2j+1 in the high nibble (q in 0..15).
+ *                sc0 = scales_zeros bf16 [K/group][N][2] = (s, z);
+ *                w_eff = (q - 8) * s + z.   This is the byte layout of the
+ *                rebuilt Int4Linear.weight_int4 and the exact scales_zeros of
+ *                models/int4_linear.py:61-63.
+ * BZ_W_INT4_MIN: same nibbles; sc0 = scale bf16 [N][K/group], sc1 = min bf16
+ *                [N][K/group]; w_eff = q * s + min
+ *                (models/fused/kernels.py:141-150, FusedWeight bits=4).
+ * BZ_W_FP8     : w uint8 [N][K] OCP e4m3 ("e4m3fn") codes; sc0 = float
+ *                [N] per-output-channel scale, applied to the fp32 dot
+ *                product (models/fused/kernels.py:124-126,133-134;
+ *                Fp8Linear.weight_fp8 / weight_scale, models/fp8_linear.py:62-66).
+ * BZ_W_BF16    : w bf16 [N][K]; sc0/sc1 unused (FusedWeight bits=16).
+ */
+typedef enum bz_wfmt {
+    BZ_W_INT4_ZP = 0,
+    BZ_W_INT4_MIN = 1,
+    BZ_W_FP8 = 2,
+    BZ_W_BF16 = 3
+} bz_wfmt;
+
+/* Epilogues of models/fused/kernels.py:8-13 (EPI 0/1/2). */
+typedef enum bz_epilogue {
+    BZ_EPI_NONE = 0,
+    BZ_EPI_SILU_GATE = 1,  /* out[m,j] = silu(acc[m,j]) * acc[m,j+N/2]; N_out = N/2 */
+    BZ_EPI_RESIDUAL = 2    /* out[m,n] = acc[m,n] + residual[m,n]                   */
+} bz_epilogue;
+
+typedef enum bz_dtype {
+    BZ_DT_BF16 = 0,
+    BZ_DT_F32 = 1
+} bz_dtype;
+
+/* One GEMV call: out[M, N_out] = epilogue( rmsnorm(x) @ w_eff^T ).
+ *
+ * x is bf16 [M][ldx] (ldx >= K, x and every row 16-byte aligned: ldx % 8 == 0).
+ * gamma (bf16 [K]) != NULL enables the RMSNorm prologue
+ *   x_hat = bf16(x * rsqrt(mean(x^2) + eps) * gamma)   (fp32 math),
+ * computed inside the kernel from the full row of x
+ * (models/fused/kernels.py:65-81).  Accumulation is fp32.
+ * residual (dtype residual_dtype, [M][ldr]) is read only for BZ_EPI_RESIDUAL
+ * and may alias `out`.  out is [M][ldo] of out_dtype.
+ * cfg_nch / cfg_nw: 0 selects the built-in per-shape table; otherwise they
+ * force the chunks-per-wave (2, 4 or 8) and waves-per-workgroup (1..16) of the
+ * streaming kernel (used by tuning sweeps).
+ */
+typedef struct bz_gemv_desc {
+    int32_t abi_version;      /* must be BZ_ABI_VERSION */
+    int32_t M, N, K;          /* N = weight rows (2*N_out for SiLU-gate) */
+    int32_t group;            /* int4 group size (power of two >= 32) */
+    int32_t wfmt;             /* bz_wfmt */
+    int32_t epilogue;         /* bz_epilogue */
+    int32_t out_dtype;        /* bz_dtype */
+    int32_t residual_dtype;   /* bz_dtype */
+    int32_t cfg_nch, cfg_nw;  /* 0 = automatic */
+    float eps;
+    const void* x;  int64_t ldx;
+    const void* w;
+    const void* sc0;
+    const void* sc1;
+    const void* gamma;
+    const void* residual; int64_t ldr;
+    void* out; int64_t ldo;
+    void* workspace; size_t workspace_bytes;  /* reserved: current kernels need none */
+} bz_gemv_desc;
+
+/* ABI version of the loaded library (BZ_ABI_VERSION it was built with). */
+int bz_abi_version(void);
+
+/* Static description of a status code. */
+const char* bz_strerror(int status);
+
+/* Workspace bytes bz_gemv needs for this descriptor (0 for every shape the
+ * current kernels run: split-K partials never leave the workgroup). */
+size_t bz_gemv_workspace(const bz_gemv_desc* d);
+
+/* The fused decode GEMV.  Replaces, as one launch:
+ *   rms_gemv + _launch (rms_gemv_kernel + gemv_epilogue_kernel)
+ *       models/fused/kernels.py:201-219, 334-351
+ *   torch._weight_int4pack_mm in Int4Linear.forward
+ *       models/int4_linear.py:103-108
+ *   torch._scaled_mm in Fp8Linear.forward (weight-only form, bf16
+ *       activations) models/fp8_linear.py:76-82
+ * Any M >= 1 is accepted (the reference fused kernel stops at M <= 2,
+ * models/fused/kernels.py:336). */
+int bz_gemv(const bz_gemv_desc* d, void* stream);
+
+/* Row RMSNorm, out = bf16(x * rsqrt(mean(x^2)+eps) * gamma); bf16 in/out.
+ * Replaces rmsnorm / rmsnorm_kernel, models/fused/kernels.py:541-557. */
+int bz_rmsnorm(const void* x, int64_t ldx, const void* gamma, float eps,
+               void* out, int64_t ldo, int32_t M, int32_t K, void* stream);
+
+/* out = silu(g) * u, bf16 in/out.
+ * Replaces silu_mul / silu_mul_kernel, models/fused/kernels.py:560-575. */
+int bz_silu_mul(const void* g, int64_t ldg, const void* u, int64_t ldu,
+                void* out, int64_t ldo, int32_t M, int32_t N, void* stream);
+
+/* Group int4 quantizer (load time).  w is [N][K] float32 (w_dtype BZ_DT_F32)
+ * or bf16 (BZ_DT_BF16).  symmetric = 0: min/max quantizer of
+ * quantize_int4 (models/int4_linear.py:47-63) and pack_int4
+ * (models/fused/kernels.py:141-150); symmetric = 1: s = absmax/7,
+ * q = clamp(rne(w/s)+8, 0, 15), z = 0.
+ * Writes packed uint8 [N][K/2] (even-k low nibble) and, for
+ * layout BZ_W_INT4_ZP, sc0 = scales_zeros bf16 [K/group][N][2];
+ * for BZ_W_INT4_MIN, sc0 = scale bf16 [N][K/group], sc1 = min bf16.
+ * Replaces quantize_int4 + torch._convert_weight_to_int4pack
+ * (models/int4_linear.py:47-64) and pack_int4. */
+int bz_quantize_int4(const void* w, int32_t w_dtype, int32_t N, int32_t K,
+                     int32_t group, int32_t symmetric, int32_t layout,
+                     void* packed, void* sc0, void* sc1, void* stream);
+
+/* Per-output-channel fp8 e4m3 quantizer (load time): scale = max(amax,
+ * amax_floor)/448, code = e4m3(clamp(w/scale, -448, 448)) with round to
+ * nearest even.  amax_floor = 1e-12 is Fp8Linear.__init__
+ * (models/fp8_linear.py:58-62); 1e-8 is pack_fp8
+ * (models/fused/kernels.py:153-158).  Writes codes uint8 [N][K] and
+ * scale float [N]. */
+int bz_quantize_fp8(const void* w, int32_t w_dtype, int32_t N, int32_t K,
+                    float amax_floor, void* codes, void* scale, void* stream);
+
+/* Dequantize any weight format to float [N][K] (w_eff of bench_gemv.py:47-52)
+ * with the same device unpacking code as bz_gemv.  Used to pin unpacking and
+ * indexing bit-exactly, and for checkpoint export. */
+int bz_dequant(int32_t wfmt, const void* w, const void* sc0, const void* sc1,
+               int32_t N, int32_t K, int32_t group, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BZ_GEMV_H */

@@ -1,0 +1,263 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle.
+
+Bars (stated by the task's north star):
+  * unpacking, indexing and quantization: bit-exact;
+  * GEMV outputs (bf16, fp32 accumulation): max|out-ref|/max|ref| <= 1e-2,
+    the metric of bench_gemv.py:53.  The oracle reference is float64
+    dequantize-then-matmul on the same packed weights (bench_gemv.py:30-52).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bz_oracle as O
+from tests._util import Fp8Case, Int4Case, bf16_bits, bf16_tensor, f32, u8_tensor
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2          # the stated bar
+TIGHT = 4e-3        # against the same-rounding oracle: catches dropped terms
+
+from breeze_amd import gemv as G  # noqa: E402
+
+
+def _dev():
+    return torch.device("cuda", 0)
+
+
+# ---------------------------------------------------------------------------
+# decoders: bit-exact
+# ---------------------------------------------------------------------------
+
+
+def test_fp8_decode_all_codes_bit_exact():
+    """All 256 e4m3 codes through the GEMV's conversion (scale 1)."""
+    codes = np.arange(256, dtype=np.uint8).reshape(16, 16)
+    got = f32(G.dequant(G.W_FP8, u8_tensor(codes), 16, 16, sc0=torch.ones(16, device=_dev())))
+    want = O.e4m3fn_decode(codes)
+    finite = ~np.isnan(want)
+    assert np.array_equal(got[finite].view(np.uint32), want[finite].view(np.uint32))
+    assert np.isnan(got[~finite]).all()
+
+
+@pytest.mark.parametrize("layout", ["zp", "min"])
+@pytest.mark.parametrize("group", [32, 64, 128, 256])
+def test_int4_dequant_bit_exact(layout, group):
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((24, 512)) * 0.02).astype(np.float32)
+    c = Int4Case(w, group)
+    if layout == "zp":
+        got = f32(G.dequant(G.W_INT4_ZP, c.d_packed, c.N, c.K, sc0=c.d_sz, group=group))
+        want = c.w_zp
+    else:
+        got = f32(G.dequant(G.W_INT4_MIN, c.d_packed, c.N, c.K, sc0=c.d_s, sc1=c.d_m, group=group))
+        want = c.w_min
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_int4_single_nibble_sweep():
+    """One non-zero nibble at every k of a row: pins k -> (byte, nibble)."""
+    K = 256
+    q = np.zeros((K, K), dtype=np.uint8)
+    q[np.arange(K), np.arange(K)] = np.arange(K) % 15 + 1
+    packed = O.pack_nibbles_even_low(q)
+    sz = O.scales_zeros(np.ones((K, K // 128), np.float32), np.zeros((K, K // 128), np.float32))
+    got = f32(G.dequant(G.W_INT4_ZP, u8_tensor(packed), K, K, sc0=bf16_tensor(sz), group=128))
+    want = q.astype(np.float32) - 8.0
+    assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------------------------
+# quantizers: bit-exact against the oracle restatement
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("symmetric", [False, True])
+@pytest.mark.parametrize("wdtype", ["f32", "bf16"])
+def test_quantize_int4_bit_exact(symmetric, wdtype):
+    rng = np.random.default_rng(2)
+    w = (rng.standard_normal((64, 1024)) * 0.02).astype(np.float32)
+    w[3, :128] = 0.5          # constant group: scale floor
+    w[5, 128:256] = np.linspace(-1, 1, 128, dtype=np.float32)
+    if wdtype == "bf16":
+        w = O.round_bf16(w)
+        wt = bf16_tensor(O.f32_to_bf16_bits(w))
+    else:
+        wt = torch.from_numpy(w).to(_dev())
+    c = Int4Case(w, 128, symmetric, device="cpu")
+    packed, sz, _ = G.quantize_int4_device(wt, 128, symmetric, G.W_INT4_ZP)
+    assert np.array_equal(packed.cpu().numpy(), c.packed)
+    assert np.array_equal(bf16_bits(sz), c.sz_bits)
+    packed2, s, m = G.quantize_int4_device(wt, 128, symmetric, G.W_INT4_MIN)
+    assert np.array_equal(packed2.cpu().numpy(), c.packed)
+    assert np.array_equal(bf16_bits(s), c.s_bits)
+    assert np.array_equal(bf16_bits(m), c.m_bits)
+
+
+@pytest.mark.parametrize("floor", [1e-12, 1e-8])
+def test_quantize_fp8_bit_exact(floor):
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal((64, 512)) * 0.02).astype(np.float32)
+    w[0] = 0.0                                 # amax floor
+    w[1, :] = np.float32(1e-9)                 # tiny row
+    w[2, ::7] = 3.0                            # outliers -> subnormal codes elsewhere
+    codes, scale = G.quantize_fp8_device(torch.from_numpy(w).to(_dev()), floor)
+    want_codes, want_scale = O._fp8_quant(w, floor)
+    assert np.array_equal(scale.cpu().numpy().view(np.uint32), want_scale.view(np.uint32))
+    assert np.array_equal(codes.view(torch.uint8).cpu().numpy(), want_codes)
+
+
+# ---------------------------------------------------------------------------
+# GEMV parity
+# ---------------------------------------------------------------------------
+
+
+def _xn(x_bits, gamma_bits, norm):
+    x = O.bf16_bits_to_f32(x_bits)
+    if not norm:
+        return x, x
+    g = O.bf16_bits_to_f32(gamma_bits)
+    return O.rmsnorm_f32(x, g), O.rmsnorm_bf16(x, g)
+
+
+def _run_int4(c: Int4Case, x_bits, gamma_bits, layout, epi, res_bits=None, cfg=(0, 0)):
+    x = bf16_tensor(x_bits)
+    gamma = bf16_tensor(gamma_bits) if gamma_bits is not None else None
+    res = bf16_tensor(res_bits) if res_bits is not None else None
+    if layout == "zp":
+        return G.gemv(x, c.d_packed, G.W_INT4_ZP, c.N, sc0=c.d_sz, group=c.group, gamma=gamma, epilogue=epi,
+                      residual=res, cfg=cfg)
+    return G.gemv(x, c.d_packed, G.W_INT4_MIN, c.N, sc0=c.d_s, sc1=c.d_m, group=c.group, gamma=gamma,
+                  epilogue=epi, residual=res, cfg=cfg)
+
+
+def _check(got, xn_f32, xn_bf16, w_eff, epi, res=None, row_scale=None):
+    ref = O.gemv_ref(xn_f32, w_eff, epi, res, row_scale)
+    ref_same = O.gemv_ref(xn_bf16, w_eff, epi, res, row_scale)
+    out = f32(got)
+    e = O.rel_err(out, ref)
+    e_same = O.rel_err(out, ref_same)
+    assert e <= TOL, e
+    assert e_same <= TIGHT, e_same
+    return e
+
+
+@pytest.mark.parametrize("M", [1, 2])
+def test_c1_rms_int4_2048(M):
+    """RMSNorm (eps 1e-6, gamma = 1+N(0,0.1)) fused into int4 GEMV, K = N =
+    2048, group 128, symmetric int4, bf16 out."""
+    w, gamma, x = O.synth(2048, 2048, M, seed=0)
+    c = Int4Case(w, 128, symmetric=True)
+    got = _run_int4(c, x, gamma, "zp", G.EPI_NONE)
+    a, b = _xn(x, gamma, True)
+    _check(got, a, b, c.w_zp, O.EPI_NONE)
+
+
+@pytest.mark.parametrize("layout", ["zp", "min"])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("epi", [0, 1, 2])
+@pytest.mark.parametrize("norm", [False, True])
+def test_int4_gemv_small(layout, M, epi, norm):
+    N, K = 272, 768   # ragged: N/8 tiles with a partial SiLU tile; K = 3 chunks
+    w, gamma, x = O.synth(N, K, M, seed=M * 7 + epi)
+    c = Int4Case(w, 128)
+    n_out = N // 2 if epi == 1 else N
+    res_bits = O.f32_to_bf16_bits(np.random.default_rng(5).standard_normal((M, n_out)).astype(np.float32))
+    got = _run_int4(c, x, gamma if norm else None, layout, epi, res_bits if epi == 2 else None)
+    a, b = _xn(x, gamma, norm)
+    w_eff = c.w_zp if layout == "zp" else c.w_min
+    _check(got, a, b, w_eff, epi, O.bf16_bits_to_f32(res_bits) if epi == 2 else None)
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 6])
+@pytest.mark.parametrize("epi", [0, 1, 2])
+@pytest.mark.parametrize("norm", [False, True])
+def test_fp8_gemv_small(M, epi, norm):
+    N, K = 264, 1040   # K = 8 full chunks + a 16-byte tail
+    w, gamma, x = O.synth(N, K, M, seed=11 + M)
+    c = Fp8Case(w)
+    n_out = N // 2 if epi == 1 else N
+    res_bits = O.f32_to_bf16_bits(np.random.default_rng(6).standard_normal((M, n_out)).astype(np.float32))
+    got = G.gemv(bf16_tensor(x), c.d_codes, G.W_FP8, N, sc0=c.d_scale, gamma=bf16_tensor(gamma) if norm else None,
+                 epilogue=epi, residual=bf16_tensor(res_bits) if epi == 2 else None)
+    a, b = _xn(x, gamma, norm)
+    w8 = O.e4m3fn_decode(c.codes)
+    _check(got, a, b, w8, epi, O.bf16_bits_to_f32(res_bits) if epi == 2 else None, row_scale=c.scale)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3])
+@pytest.mark.parametrize("epi", [0, 1, 2])
+def test_bf16_gemv_small(M, epi):
+    N, K = 136, 520
+    w, gamma, x = O.synth(N, K, M, seed=21 + M)
+    wb = O.f32_to_bf16_bits(w)
+    n_out = N // 2 if epi == 1 else N
+    res_bits = O.f32_to_bf16_bits(np.random.default_rng(7).standard_normal((M, n_out)).astype(np.float32))
+    got = G.gemv(bf16_tensor(x), bf16_tensor(wb), G.W_BF16, N, gamma=bf16_tensor(gamma), epilogue=epi,
+                 residual=bf16_tensor(res_bits) if epi == 2 else None)
+    a, b = _xn(x, gamma, True)
+    _check(got, a, b, O.bf16_bits_to_f32(wb), epi, O.bf16_bits_to_f32(res_bits) if epi == 2 else None)
+
+
+def test_int4_gemv_one_hot_bit_exact():
+    """x = e_k with dyadic scales: every output is exactly w_eff[:, k]; any
+    nibble-order, group-index or row-mapping slip changes bits."""
+    N, K, group = 64, 512, 128
+    rng = np.random.default_rng(9)
+    q = rng.integers(0, 16, (N, K), dtype=np.uint8)
+    s = (2.0 ** rng.integers(-8, -4, (N, K // group))).astype(np.float32)
+    z = (rng.integers(-64, 64, (N, K // group)) * 2.0 ** -9).astype(np.float32)
+    sz = O.scales_zeros(s, z)
+    w_eff = O.dequant_int4_zp(q, sz, group)
+    d_w, d_sz = u8_tensor(O.pack_nibbles_even_low(q)), bf16_tensor(sz)
+    ks = list(range(0, K, 37)) + [K - 1]
+    x = np.zeros((len(ks), K), np.float32)
+    x[np.arange(len(ks)), ks] = 1.0
+    for m0 in range(0, len(ks), 4):
+        xb = O.f32_to_bf16_bits(x[m0:m0 + 4])
+        got = f32(G.gemv(bf16_tensor(xb), d_w, G.W_INT4_ZP, N, sc0=d_sz, group=group, out_dtype=torch.float32))
+        for i, k in enumerate(ks[m0:m0 + 4]):
+            assert np.array_equal(got[i], w_eff[:, k]), k
+
+
+def test_fp8_gemv_one_hot_bit_exact():
+    N, K = 64, 256
+    rng = np.random.default_rng(10)
+    codes = rng.integers(0, 256, (N, K), dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x10          # no NaN codes
+    scale = np.ones(N, np.float32)
+    want = O.e4m3fn_decode(codes)
+    ks = [0, 1, 2, 3, 15, 16, 17, 100, 255]
+    x = np.zeros((len(ks), K), np.float32)
+    x[np.arange(len(ks)), ks] = 1.0
+    for m0 in range(0, len(ks), 4):
+        got = f32(G.gemv(bf16_tensor(O.f32_to_bf16_bits(x[m0:m0 + 4])), u8_tensor(codes), G.W_FP8, N,
+                         sc0=torch.from_numpy(scale).cuda(), out_dtype=torch.float32))
+        for i, k in enumerate(ks[m0:m0 + 4]):
+            assert np.array_equal(got[i], want[:, k]), k
+
+
+@pytest.mark.parametrize("nch,nw", [(2, 1), (2, 7), (4, 3), (8, 1), (8, 16), (4, 16)])
+def test_launch_shapes_agree(nch, nw):
+    """Every forced (chunks-per-wave, waves) shape gives the same result."""
+    N, K = 512, 2560
+    w, gamma, x = O.synth(N, K, 2, seed=4)
+    c = Int4Case(w)
+    base = f32(_run_int4(c, x, gamma, "zp", G.EPI_SILU_GATE))
+    got = f32(_run_int4(c, x, gamma, "zp", G.EPI_SILU_GATE, cfg=(nch, nw)))
+    a, b = _xn(x, gamma, True)
+    assert O.rel_err(got, O.gemv_ref(b, c.w_zp, O.EPI_SILU)) <= TIGHT
+    assert O.rel_err(got, base) <= TIGHT
+
+
+def test_errors_raise():
+    x = torch.zeros(1, 100, dtype=torch.bfloat16, device=_dev())
+    w = torch.zeros(8, 50, dtype=torch.uint8, device=_dev())
+    sz = torch.zeros(1, 8, 2, dtype=torch.bfloat16, device=_dev())
+    with pytest.raises(RuntimeError, match="unsupported shape"):
+        G.gemv(x, w, G.W_INT4_ZP, 8, sc0=sz, group=128)
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        G.gemv(torch.zeros(1, 128, dtype=torch.bfloat16, device=_dev()), w, G.W_INT4_ZP, 8, group=128)
