@@ -48,8 +48,10 @@ class GemvDesc(ctypes.Structure):
         ("epilogue", ctypes.c_int32),
         ("out_dtype", ctypes.c_int32),
         ("residual_dtype", ctypes.c_int32),
-        ("cfg_nch", ctypes.c_int32),
-        ("cfg_nw", ctypes.c_int32),
+        ("cfg_depth", ctypes.c_int32),
+        ("cfg_waves", ctypes.c_int32),
+        ("cfg_tiles", ctypes.c_int32),
+        ("cfg_path", ctypes.c_int32),
         ("eps", ctypes.c_float),
         ("x", ctypes.c_void_p),
         ("ldx", ctypes.c_int64),

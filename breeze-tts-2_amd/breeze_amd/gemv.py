@@ -88,7 +88,7 @@ def gemv(
     residual: Optional[torch.Tensor] = None,
     out: Optional[torch.Tensor] = None,
     out_dtype: torch.dtype = torch.bfloat16,
-    cfg: tuple[int, int] = (0, 0),
+    cfg: tuple = (0, 0, 0, 0),
 ) -> torch.Tensor:
     """out[M, N_out] = epilogue(rmsnorm?(x) @ w_eff^T) in one launch.
 
@@ -138,7 +138,7 @@ def gemv(
     d.epilogue = epilogue
     d.out_dtype = _DT[out.dtype]
     d.residual_dtype = res_dt
-    d.cfg_nch, d.cfg_nw = cfg
+    d.cfg_depth, d.cfg_waves, d.cfg_tiles, d.cfg_path = (tuple(cfg) + (0, 0, 0, 0))[:4]
     d.eps = eps
     d.x, d.ldx = x.data_ptr(), x.stride(0)
     d.w = w.data_ptr()

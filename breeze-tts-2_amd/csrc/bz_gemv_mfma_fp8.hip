@@ -1,0 +1,6 @@
+// Matrix-core instances of the streaming GEMV for one weight format (WF_FP8).
+#include "bz_gemv_mfma.h"
+
+namespace bz {
+int launch_mfma_fp8(const GemvParams& p, const Launch& l, hipStream_t st) { return launch_mfma_m<WF_FP8>(p, l, st); }
+}  // namespace bz

@@ -1,0 +1,6 @@
+// Matrix-core instances of the streaming GEMV for one weight format (WF_I4MIN).
+#include "bz_gemv_mfma.h"
+
+namespace bz {
+int launch_mfma_i4min(const GemvParams& p, const Launch& l, hipStream_t st) { return launch_mfma_m<WF_I4MIN>(p, l, st); }
+}  // namespace bz

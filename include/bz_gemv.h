@@ -76,15 +76,19 @@ typedef enum bz_dtype {
 /* One GEMV call: out[M, N_out] = epilogue( rmsnorm(x) @ w_eff^T ).
  *
  * x is bf16 [M][ldx] (ldx >= K, x and every row 16-byte aligned: ldx % 8 == 0).
- * gamma (bf16 [K]) != NULL enables the RMSNorm prologue
- *   x_hat = bf16(x * rsqrt(mean(x^2) + eps) * gamma)   (fp32 math),
- * computed inside the kernel from the full row of x
+ * gamma (bf16 [K]) != NULL enables the fused RMSNorm
+ *   out = rsqrt(mean(x^2) + eps) * (bf16(x * gamma) @ w_eff^T)   (fp32 math),
+ * i.e. rmsnorm(x) @ w_eff^T with the per-row scalar applied after the dot
+ * product, computed inside the kernel from the full row of x
  * (models/fused/kernels.py:65-81).  Accumulation is fp32.
  * residual (dtype residual_dtype, [M][ldr]) is read only for BZ_EPI_RESIDUAL
  * and may alias `out`.  out is [M][ldo] of out_dtype.
- * cfg_nch / cfg_nw: 0 selects the built-in per-shape table; otherwise they
- * force the chunks-per-wave (2, 4 or 8) and waves-per-workgroup (1..16) of the
- * streaming kernel (used by tuning sweeps).
+ * cfg_depth / cfg_waves / cfg_tiles / cfg_path: 0 selects the built-in
+ * per-shape rule; otherwise they force the streaming kernel's pipeline depth
+ * (2, 4, 8 or 16 steps of weight loads in flight per wave; at most 8 for
+ * SiLU-gate), waves per workgroup (1..8), output tiles per workgroup (>= 1)
+ * and arithmetic path (1 = v_dot2 kernel, 8-column tiles; 2 = MFMA kernel,
+ * 16-column tiles, needs an int4 group >= 128).  Used by tuning sweeps.
  */
 typedef struct bz_gemv_desc {
     int32_t abi_version;      /* must be BZ_ABI_VERSION */
@@ -94,7 +98,7 @@ typedef struct bz_gemv_desc {
     int32_t epilogue;         /* bz_epilogue */
     int32_t out_dtype;        /* bz_dtype */
     int32_t residual_dtype;   /* bz_dtype */
-    int32_t cfg_nch, cfg_nw;  /* 0 = automatic */
+    int32_t cfg_depth, cfg_waves, cfg_tiles, cfg_path;  /* 0 = automatic */
     float eps;
     const void* x;  int64_t ldx;
     const void* w;
@@ -113,7 +117,7 @@ int bz_abi_version(void);
 const char* bz_strerror(int status);
 
 /* Workspace bytes bz_gemv needs for this descriptor (0 for every shape the
- * current kernels run: split-K partials never leave the workgroup). */
+ * current kernels run: partial sums never leave the workgroup). */
 size_t bz_gemv_workspace(const bz_gemv_desc* d);
 
 /* The fused decode GEMV.  Replaces, as one launch:

@@ -304,8 +304,17 @@ def rmsnorm_f32(x, gamma, eps: float = 1e-6) -> np.ndarray:
 
 
 def rmsnorm_bf16(x, gamma, eps: float = 1e-6) -> np.ndarray:
-    """GPU-path semantics: one rounding, x_hat = bf16(x * inv_rms * gamma)."""
+    """Standalone-norm rounding: x_hat = bf16(x * inv_rms * gamma)."""
     return round_bf16(rmsnorm_f32(x, gamma, eps))
+
+
+def rmsnorm_folded(x, gamma, eps: float = 1e-6) -> np.ndarray:
+    """Rounding of the fused norm-GEMV: the product is taken against
+    u = bf16(x * gamma) and scaled by inv_rms afterwards, which equals a GEMV
+    over x_hat = u * inv_rms (fp32, no second rounding)."""
+    x = np.asarray(x, dtype=np.float32)
+    u = round_bf16(x * np.asarray(gamma, dtype=np.float32))
+    return (u * _inv_rms(x, eps)).astype(np.float32)
 
 
 def rmsnorm_model(x, gamma, eps: float = 1e-6) -> np.ndarray:

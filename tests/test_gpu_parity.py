@@ -120,7 +120,7 @@ def _xn(x_bits, gamma_bits, norm):
     if not norm:
         return x, x
     g = O.bf16_bits_to_f32(gamma_bits)
-    return O.rmsnorm_f32(x, g), O.rmsnorm_bf16(x, g)
+    return O.rmsnorm_f32(x, g), O.rmsnorm_folded(x, g)
 
 
 def _run_int4(c: Int4Case, x_bits, gamma_bits, layout, epi, res_bits=None, cfg=(0, 0)):
@@ -145,64 +145,69 @@ def _check(got, xn_f32, xn_bf16, w_eff, epi, res=None, row_scale=None):
     return e
 
 
+@pytest.mark.parametrize("path", [1, 2])
 @pytest.mark.parametrize("M", [1, 2])
-def test_c1_rms_int4_2048(M):
+def test_c1_rms_int4_2048(M, path):
     """RMSNorm (eps 1e-6, gamma = 1+N(0,0.1)) fused into int4 GEMV, K = N =
     2048, group 128, symmetric int4, bf16 out."""
     w, gamma, x = O.synth(2048, 2048, M, seed=0)
     c = Int4Case(w, 128, symmetric=True)
-    got = _run_int4(c, x, gamma, "zp", G.EPI_NONE)
+    got = _run_int4(c, x, gamma, "zp", G.EPI_NONE, cfg=(0, 0, 0, path))
     a, b = _xn(x, gamma, True)
     _check(got, a, b, c.w_zp, O.EPI_NONE)
 
 
+@pytest.mark.parametrize("path", [1, 2])
 @pytest.mark.parametrize("layout", ["zp", "min"])
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
 @pytest.mark.parametrize("epi", [0, 1, 2])
 @pytest.mark.parametrize("norm", [False, True])
-def test_int4_gemv_small(layout, M, epi, norm):
+def test_int4_gemv_small(layout, M, epi, norm, path):
     N, K = 272, 768   # ragged: N/8 tiles with a partial SiLU tile; K = 3 chunks
     w, gamma, x = O.synth(N, K, M, seed=M * 7 + epi)
     c = Int4Case(w, 128)
     n_out = N // 2 if epi == 1 else N
     res_bits = O.f32_to_bf16_bits(np.random.default_rng(5).standard_normal((M, n_out)).astype(np.float32))
-    got = _run_int4(c, x, gamma if norm else None, layout, epi, res_bits if epi == 2 else None)
+    got = _run_int4(c, x, gamma if norm else None, layout, epi, res_bits if epi == 2 else None, cfg=(0, 0, 0, path))
     a, b = _xn(x, gamma, norm)
     w_eff = c.w_zp if layout == "zp" else c.w_min
     _check(got, a, b, w_eff, epi, O.bf16_bits_to_f32(res_bits) if epi == 2 else None)
 
 
+@pytest.mark.parametrize("path", [1, 2])
 @pytest.mark.parametrize("M", [1, 2, 4, 6])
 @pytest.mark.parametrize("epi", [0, 1, 2])
 @pytest.mark.parametrize("norm", [False, True])
-def test_fp8_gemv_small(M, epi, norm):
+def test_fp8_gemv_small(M, epi, norm, path):
     N, K = 264, 1040   # K = 8 full chunks + a 16-byte tail
     w, gamma, x = O.synth(N, K, M, seed=11 + M)
     c = Fp8Case(w)
     n_out = N // 2 if epi == 1 else N
     res_bits = O.f32_to_bf16_bits(np.random.default_rng(6).standard_normal((M, n_out)).astype(np.float32))
     got = G.gemv(bf16_tensor(x), c.d_codes, G.W_FP8, N, sc0=c.d_scale, gamma=bf16_tensor(gamma) if norm else None,
-                 epilogue=epi, residual=bf16_tensor(res_bits) if epi == 2 else None)
+                 epilogue=epi, residual=bf16_tensor(res_bits) if epi == 2 else None, cfg=(0, 0, 0, path))
     a, b = _xn(x, gamma, norm)
     w8 = O.e4m3fn_decode(c.codes)
     _check(got, a, b, w8, epi, O.bf16_bits_to_f32(res_bits) if epi == 2 else None, row_scale=c.scale)
 
 
+@pytest.mark.parametrize("path", [1, 2])
 @pytest.mark.parametrize("M", [1, 2, 3])
 @pytest.mark.parametrize("epi", [0, 1, 2])
-def test_bf16_gemv_small(M, epi):
+def test_bf16_gemv_small(M, epi, path):
     N, K = 136, 520
     w, gamma, x = O.synth(N, K, M, seed=21 + M)
     wb = O.f32_to_bf16_bits(w)
     n_out = N // 2 if epi == 1 else N
     res_bits = O.f32_to_bf16_bits(np.random.default_rng(7).standard_normal((M, n_out)).astype(np.float32))
     got = G.gemv(bf16_tensor(x), bf16_tensor(wb), G.W_BF16, N, gamma=bf16_tensor(gamma), epilogue=epi,
-                 residual=bf16_tensor(res_bits) if epi == 2 else None)
+                 residual=bf16_tensor(res_bits) if epi == 2 else None, cfg=(0, 0, 0, path))
     a, b = _xn(x, gamma, True)
     _check(got, a, b, O.bf16_bits_to_f32(wb), epi, O.bf16_bits_to_f32(res_bits) if epi == 2 else None)
 
 
-def test_int4_gemv_one_hot_bit_exact():
+@pytest.mark.parametrize("path", [1, 2])
+def test_int4_gemv_one_hot_bit_exact(path):
     """x = e_k with dyadic scales: every output is exactly w_eff[:, k]; any
     nibble-order, group-index or row-mapping slip changes bits."""
     N, K, group = 64, 512, 128
@@ -218,12 +223,14 @@ def test_int4_gemv_one_hot_bit_exact():
     x[np.arange(len(ks)), ks] = 1.0
     for m0 in range(0, len(ks), 4):
         xb = O.f32_to_bf16_bits(x[m0:m0 + 4])
-        got = f32(G.gemv(bf16_tensor(xb), d_w, G.W_INT4_ZP, N, sc0=d_sz, group=group, out_dtype=torch.float32))
+        got = f32(G.gemv(bf16_tensor(xb), d_w, G.W_INT4_ZP, N, sc0=d_sz, group=group, out_dtype=torch.float32,
+                         cfg=(0, 0, 0, path)))
         for i, k in enumerate(ks[m0:m0 + 4]):
             assert np.array_equal(got[i], w_eff[:, k]), k
 
 
-def test_fp8_gemv_one_hot_bit_exact():
+@pytest.mark.parametrize("path", [1, 2])
+def test_fp8_gemv_one_hot_bit_exact(path):
     N, K = 64, 256
     rng = np.random.default_rng(10)
     codes = rng.integers(0, 256, (N, K), dtype=np.uint8)
@@ -235,22 +242,62 @@ def test_fp8_gemv_one_hot_bit_exact():
     x[np.arange(len(ks)), ks] = 1.0
     for m0 in range(0, len(ks), 4):
         got = f32(G.gemv(bf16_tensor(O.f32_to_bf16_bits(x[m0:m0 + 4])), u8_tensor(codes), G.W_FP8, N,
-                         sc0=torch.from_numpy(scale).cuda(), out_dtype=torch.float32))
+                         sc0=torch.from_numpy(scale).cuda(), out_dtype=torch.float32, cfg=(0, 0, 0, path)))
         for i, k in enumerate(ks[m0:m0 + 4]):
             assert np.array_equal(got[i], want[:, k]), k
 
 
-@pytest.mark.parametrize("nch,nw", [(2, 1), (2, 7), (4, 3), (8, 1), (8, 16), (4, 16)])
-def test_launch_shapes_agree(nch, nw):
+@pytest.mark.parametrize("path", [1, 2])
+@pytest.mark.parametrize("depth,nw,tiles", [(2, 1, 1), (2, 7, 3), (4, 3, 0), (4, 1, 64), (2, 8, 5), (8, 8, 2), (8, 2, 0)])
+def test_launch_shapes_agree_silu(depth, nw, tiles, path):
     """Every forced (chunks-per-wave, waves) shape gives the same result."""
     N, K = 512, 2560
     w, gamma, x = O.synth(N, K, 2, seed=4)
     c = Int4Case(w)
     base = f32(_run_int4(c, x, gamma, "zp", G.EPI_SILU_GATE))
-    got = f32(_run_int4(c, x, gamma, "zp", G.EPI_SILU_GATE, cfg=(nch, nw)))
+    got = f32(_run_int4(c, x, gamma, "zp", G.EPI_SILU_GATE, cfg=(depth, nw, tiles, path)))
     a, b = _xn(x, gamma, True)
     assert O.rel_err(got, O.gemv_ref(b, c.w_zp, O.EPI_SILU)) <= TIGHT
     assert O.rel_err(got, base) <= TIGHT
+
+
+@pytest.mark.parametrize("path", [1, 2])
+@pytest.mark.parametrize("fmt", ["int4", "fp8"])
+@pytest.mark.parametrize("depth,nw,tiles", [(8, 1, 1), (2, 8, 1), (4, 5, 2), (2, 3, 4), (2, 1, 7), (8, 8, 25), (16, 4, 3), (16, 8, 0)])
+def test_launch_shapes_agree_tiles(fmt, depth, nw, tiles, path):
+    """Tiles-per-workgroup and wave/chunk splits all agree (ragged N)."""
+    N, K, M = 200, 4096, 3
+    w, gamma, x = O.synth(N, K, M, seed=5)
+    res_bits = O.f32_to_bf16_bits(np.random.default_rng(8).standard_normal((M, N)).astype(np.float32))
+    if fmt == "int4":
+        c = Int4Case(w)
+        got = f32(_run_int4(c, x, None, "zp", G.EPI_RESIDUAL, res_bits, cfg=(depth, nw, tiles, path)))
+        w_eff, rs = c.w_zp, None
+    else:
+        c = Fp8Case(w)
+        got = f32(G.gemv(bf16_tensor(x), c.d_codes, G.W_FP8, N, sc0=c.d_scale, epilogue=G.EPI_RESIDUAL,
+                         residual=bf16_tensor(res_bits), cfg=(depth, nw, tiles, path)))
+        w_eff, rs = O.e4m3fn_decode(c.codes), c.scale
+    a, b = _xn(x, gamma, False)
+    _check(torch.from_numpy(got), a, b, w_eff, O.EPI_RES, O.bf16_bits_to_f32(res_bits), row_scale=rs)
+
+
+def test_mfma_path_needs_group_128():
+    w, gamma, x = O.synth(64, 512, 1, seed=6)
+    c = Int4Case(w, 64)
+    with pytest.raises(RuntimeError, match="exceeds what this build supports"):
+        _run_int4(c, x, gamma, "zp", G.EPI_NONE, cfg=(0, 0, 0, 2))
+    got = f32(_run_int4(c, x, gamma, "zp", G.EPI_NONE))  # auto path: dot2 kernel
+    a, b = _xn(x, gamma, True)
+    assert O.rel_err(got, O.gemv_ref(b, c.w_zp)) <= TIGHT
+
+
+def test_invalid_launch_shape_rejected():
+    N, K = 64, 512
+    w, gamma, x = O.synth(N, K, 1, seed=6)
+    c = Int4Case(w)
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        _run_int4(c, x, gamma, "zp", G.EPI_SILU_GATE, cfg=(16, 1, 0))
 
 
 def test_errors_raise():
