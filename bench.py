@@ -1,0 +1,405 @@
+#!/usr/bin/env python3
+"""Decode-GEMV benchmark on one MI355X.
+
+Workload (the int4 decoder-MLP GEMVs at M = 1): every step runs
+  gate|up  RMSNorm -> int4 group-128 GEMV K=2560, N=2x10240 -> SiLU(gate)*up
+  down     int4 group-128 GEMV K=10240, N=2560
+on synthetic weights N(0, 0.02) quantized symmetric int4 (bf16 scales), bf16
+activations N(0, 1), gamma = 1 + N(0, 0.1), eps 1e-6, seed 0.  The weights
+rotate over copies spanning >= 1 GiB so every step streams them from HBM,
+and the K timed steps are one HIP-graph replay.
+
+value = algorithmic bytes of K steps / their GPU time, in TB/s, where one
+call's algorithmic bytes are packed weights + scales + x + gamma + output
+(each byte once, no re-reads).  Also reported:
+  roofline     the gate|up GEMV alone (the dominant kernel): its average
+               launch duration from HIP events on its launch stream, and the
+               HBM bytes per launch measured by rocprofv3 counters when a
+               committed summary holds them;
+  cpu_baseline the same MLP step as dequantize-then-matmul in torch on the
+               host cores (a bounded sample of steps);
+  detail       per-kernel times and the full synthetic decode step
+               (26 int4 decoder layers + bf16 head) in µs against its
+               bytes-moved roofline.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-step]
+
+Counter runs (HBM bytes per launch of the gate|up GEMV, scaled by what the
+same counter reads for a plain 256 MiB elementwise copy):
+  rocprofv3 --pmc FETCH_SIZE --output-format csv -d D1 -o run -- python3 bench.py --profile-gateup
+  rocprofv3 --pmc WRITE_SIZE --output-format csv -d D2 -o run -- python3 bench.py --profile-gateup
+  python3 bench.py --pmc-summary D1 D2      (prints the traffic summary)
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "breeze-tts-2_amd"))
+
+HBM_PEAK_GBPS = 8000.0
+GROUP = 128
+EPS = 1e-6
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_int4_gateup_k2560_n20480_m1_traffic.txt")
+COPY_BYTES = 256 << 20
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def algo_bytes(wbits: int, n: int, k: int, m: int, norm: bool, epi: int) -> int:
+    """Algorithmic bytes of one GEMV call: weights + scales + x (+ gamma)
+    + output (+ residual); SiLU-gate halves the output."""
+    if wbits == 4:
+        w = n * k // 2 + (k // GROUP) * n * 4
+    elif wbits == 8:
+        w = n * k + 4 * n
+    else:
+        w = 2 * n * k
+    n_out = n // 2 if epi == 1 else n
+    return w + 2 * m * k + (2 * k if norm else 0) + 2 * m * n_out + (2 * m * n_out if epi == 2 else 0)
+
+
+def read_traffic():
+    """HBM bytes per launch of the gate|up GEMV from the committed rocprofv3
+    counter summary (line 'traffic_bytes_per_launch: <int>'), else None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                m = re.match(r"\s*traffic_bytes_per_launch:\s*(\d+)", line)
+                if m:
+                    return int(m.group(1))
+    except OSError:
+        pass
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-step", action="store_true", help="skip the 26-layer decode step detail")
+    ap.add_argument("--profile-gateup", action="store_true",
+                    help="only launch the gate|up GEMV (eagerly) and a 256 MiB copy, for counter runs")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="summarize two rocprofv3 --pmc runs of --profile-gateup")
+    args = ap.parse_args()
+    if args.pmc_summary:
+        return pmc_summary(*args.pmc_summary)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the decode GEMVs here run "
+              "on a single MI355X and no multi-GPU path is built).", file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from breeze_amd import gemv as G
+    from breeze_amd import _lib
+
+    _lib.lib()  # fails loudly when the HIP library is missing
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (torch.cuda.is_available() is False)", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    log(f"device {torch.cuda.get_device_name(0)}")
+
+    # ---- synthetic C2 weights (seed 0: W, then gamma, then x, on the CPU)
+    K1, N1, K2, N2, M = 2560, 20480, 10240, 2560, 1
+    torch.manual_seed(0)
+    w_gu = torch.randn(N1, K1) * 0.02
+    w_dn = torch.randn(N2, K2) * 0.02
+    gamma = (1 + 0.1 * torch.randn(K1)).to(torch.bfloat16)
+    x = torch.randn(M, K1).to(torch.bfloat16)
+    gu_p, gu_sz, _ = G.quantize_int4_device(w_gu.to(dev), GROUP, True, G.W_INT4_ZP)
+    dn_p, dn_sz, _ = G.quantize_int4_device(w_dn.to(dev), GROUP, True, G.W_INT4_ZP)
+    del w_gu, w_dn
+    gamma_d, x_d = gamma.to(dev), x.to(dev)
+    b_gu = algo_bytes(4, N1, K1, M, True, 1)
+    b_dn = algo_bytes(4, N2, K2, M, False, 0)
+    step_bytes = b_gu + b_dn
+    wbytes = sum(t.numel() * t.element_size() for t in (gu_p, gu_sz, dn_p, dn_sz))
+    ncopy = max(2, -(-(1 << 30) // wbytes))
+    copies = [(gu_p.clone(), gu_sz.clone(), dn_p.clone(), dn_sz.clone()) for _ in range(ncopy)]
+    h = torch.empty(M, N1 // 2, device=dev, dtype=torch.bfloat16)
+    y = torch.empty(M, N2, device=dev, dtype=torch.bfloat16)
+    log(f"C2 M={M}: {ncopy} weight copies ({ncopy * wbytes / 2**30:.2f} GiB), {step_bytes} algorithmic bytes/step")
+
+    def gate_up(c):
+        G.gemv(x_d, c[0], G.W_INT4_ZP, N1, sc0=c[1], group=GROUP, gamma=gamma_d, eps=EPS,
+               epilogue=G.EPI_SILU_GATE, out=h)
+
+    def down(c):
+        G.gemv(h, c[2], G.W_INT4_ZP, N2, sc0=c[3], group=GROUP, out=y)
+
+    def step(i):
+        c = copies[i % ncopy]
+        gate_up(c)
+        down(c)
+
+    def capture(fn, n):
+        st = torch.cuda.Stream()
+        st.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(st):
+            with torch.cuda.graph(g, stream=st):
+                for i in range(n):
+                    fn(i)
+        torch.cuda.current_stream().wait_stream(st)
+        torch.cuda.synchronize()
+        return g
+
+    def timed(g):
+        """Replay g once between synchronizations; returns (event ms, wall s)."""
+        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        s_ev.record()
+        g.replay()
+        e_ev.record()
+        torch.cuda.synchronize()
+        return s_ev.elapsed_time(e_ev), time.perf_counter() - t0
+
+    if args.profile_gateup:
+        for i in range(4 * ncopy):
+            gate_up(copies[i % ncopy])
+        a_cp = torch.ones(COPY_BYTES // 4, device=dev)
+        b_cp = torch.empty_like(a_cp)
+        for _ in range(3):
+            torch.mul(a_cp, 1.0, out=b_cp)
+        torch.cuda.synchronize()
+        log(f"profile run done: {4 * ncopy} gate|up launches, 3 copies of {COPY_BYTES} bytes")
+        return 0
+
+    # ---- eager check of one step against a dequantize-then-matmul on the GPU
+    step(0)
+    torch.cuda.synchronize()
+    xn = x_d.float() * torch.rsqrt(x_d.float().pow(2).mean(-1, keepdim=True) + EPS) * gamma_d.float()
+    a = xn @ G.dequant(G.W_INT4_ZP, gu_p, N1, K1, sc0=gu_sz, group=GROUP).float().t()
+    ref_h = torch.nn.functional.silu(a[:, : N1 // 2]) * a[:, N1 // 2:]
+    err_h = ((h.float() - ref_h).abs().max() / ref_h.abs().max()).item()
+    ref_y = h.float() @ G.dequant(G.W_INT4_ZP, dn_p, N2, K2, sc0=dn_sz, group=GROUP).float().t()
+    err_y = ((y.float() - ref_y).abs().max() / ref_y.abs().max()).item()
+    del a, ref_h, ref_y, xn
+    log(f"parity vs dequantize-then-matmul: gate|up {err_h:.2e}, down {err_y:.2e}")
+    if not (err_h <= 1e-2 and err_y <= 1e-2):
+        print(f"parity check failed: gate|up {err_h}, down {err_y}", file=sys.stderr)
+        return 1
+
+    # ---- warm-up W steps, then exactly K timed steps (one graph replay each)
+    if args.warmup:
+        gw = capture(step, args.warmup)
+        timed(gw)
+        del gw
+    log(f"capturing {args.steps} steps")
+    gk = capture(step, args.steps)
+    ms, wall = timed(gk)
+    log(f"{args.steps} steps: {ms:.3f} ms (events), {wall * 1e3:.3f} ms (wall)")
+    del gk
+    value_tbps = step_bytes * args.steps / (ms * 1e-3) / 1e12
+
+    # ---- dominant kernel alone: gate|up, back-to-back launches on one stream
+    reps = 4 * ncopy
+    g_gu = capture(lambda i: gate_up(copies[i % ncopy]), reps)
+    timed(g_gu)
+    ms_gu, _ = timed(g_gu)
+    del g_gu
+    us_gu = ms_gu * 1e3 / reps
+    g_dn = capture(lambda i: down(copies[i % ncopy]), reps)
+    timed(g_dn)
+    ms_dn, _ = timed(g_dn)
+    del g_dn
+    us_dn = ms_dn * 1e3 / reps
+    achieved = b_gu / (us_gu * 1e-6) / 1e9
+    traffic = read_traffic()
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                "kernel": "gemv_persist int4-zp SiLU-gate K2560 N20480 M1 (+RMSNorm)",
+                "algorithmic_bytes": b_gu, "avg_launch_us": round(us_gu, 3)}
+    log(f"gate|up {us_gu:.2f} us ({achieved:.0f} GB/s), down {us_dn:.2f} us "
+        f"({b_dn / us_dn / 1e3:.0f} GB/s)")
+    del copies
+    torch.cuda.empty_cache()
+
+    detail = {
+        "gate_up_us": round(us_gu, 3), "down_us": round(us_dn, 3),
+        "down_gbps": round(b_dn / us_dn / 1e3, 1),
+        "step_roofline_us": round(step_bytes / HBM_PEAK_GBPS / 1e3, 3),
+        "parity_rel_err": {"gate_up": err_h, "down": err_y},
+    }
+
+    # ---- full synthetic decode step (26 int4 layers + bf16 head), M = 1
+    if not args.no_step:
+        detail["decode_step"] = decode_step(torch, G, dev, log)
+
+    # ---- CPU baseline: same MLP step on the host cores (bounded sample)
+    cpu = None
+    if not args.no_cpu:
+        sys.path.insert(0, ROOT)
+        from oracle.cpu_baseline import time_mlp_steps
+
+        log(f"CPU baseline: about {args.cpu_seconds:.0f} s of host work")
+        r = time_mlp_steps(x, gamma, (gu_p.cpu(), gu_sz.cpu()), (dn_p.cpu(), dn_sz.cpu()), GROUP, step_bytes,
+                           budget_s=args.cpu_seconds)
+        cpu = {"value": r["tbps"], "unit": "TB/s", "cores": r["threads"], "kind": "port",
+               "sample": f"{r['steps']} full C2 M=1 MLP steps (RMSNorm, int4 gate|up dequant+matmul, SiLU, "
+                         f"int4 down dequant+matmul) in torch fp32 on {r['threads']} threads of {r['cpu']}, "
+                         f"24 rotated weight copies",
+               "us_per_step": round(r["us_per_step"], 1)}
+        log(f"CPU: {r['us_per_step']:.0f} us/step on {r['threads']} threads")
+
+    out = {
+        "metric": "int4/fp8 GEMV achieved HBM TB/s at M=1; µs per decoder-layer decode step",
+        "value": round(value_tbps, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "int4 group-128 decoder-MLP GEMVs, M=1: RMSNorm->gate|up K2560 N2x10240 "
+                               "SiLU-gate, then down K10240 N2560",
+                   "weights": "int4 symmetric g128 (bf16 scales), bf16 activations, fp32 accumulate",
+                   "M": 1, "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "detail": detail,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def pmc_summary(fetch_dir: str, write_dir: str) -> int:
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the gate|up GEMV from
+    two rocprofv3 counter runs of --profile-gateup, each scaled by the ratio
+    of the known bytes of the 256 MiB copy to what the counter read for it."""
+    import csv
+    import glob
+    import statistics
+
+    def load(d, counter):
+        paths = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        if not paths:
+            raise SystemExit(f"no counter_collection.csv under {d}")
+        per = {}
+        for row in csv.DictReader(open(paths[0])):
+            if row["Counter_Name"] != counter:
+                continue
+            key = row["Dispatch_Id"]
+            per.setdefault(key, [row["Kernel_Name"], 0.0])[1] += float(row["Counter_Value"])
+        gemv = [v for n, v in per.values() if "gemv_persist" in n or "gemv_mfma" in n]
+        copy = [v for n, v in per.values() if "elementwise" in n.lower() and "mul" in n.lower()]
+        if len(gemv) < 8 or not copy:
+            raise SystemExit(f"{d}: {len(gemv)} GEMV and {len(copy)} copy dispatches found")
+        return statistics.median(gemv[4:]), statistics.median(copy), len(gemv)
+
+    f_gemv, f_copy, n_f = load(fetch_dir, "FETCH_SIZE")
+    w_gemv, w_copy, n_w = load(write_dir, "WRITE_SIZE")
+    kib = COPY_BYTES / 1024
+    fr, wr = kib / f_copy, kib / w_copy
+    traffic = int(round((f_gemv * fr + w_gemv * wr) * 1024))
+    b_gu = algo_bytes(4, 20480, 2560, 1, True, 1)
+    print(f"kernel: gemv int4-zp SiLU-gate K2560 N20480 M1 (+RMSNorm), median of {n_f - 4} / {n_w - 4} dispatches")
+    print(f"FETCH_SIZE per launch (KiB, raw): {f_gemv:.1f}")
+    print(f"WRITE_SIZE per launch (KiB, raw): {w_gemv:.1f}")
+    print(f"copy kernel {COPY_BYTES} B: FETCH_SIZE {f_copy:.1f} KiB -> read scale {fr:.4f}; "
+          f"WRITE_SIZE {w_copy:.1f} KiB -> write scale {wr:.4f}")
+    print(f"fetch_bytes_per_launch: {int(round(f_gemv * fr * 1024))}")
+    print(f"write_bytes_per_launch: {int(round(w_gemv * wr * 1024))}")
+    print(f"traffic_bytes_per_launch: {traffic}")
+    print(f"algorithmic_bytes_per_launch: {b_gu}")
+    print(f"traffic / algorithmic: {traffic / b_gu:.4f}")
+    return 0
+
+
+def decode_step(torch, G, dev, log) -> dict:
+    """26 decoder layers (hidden 2560, 16x256 q heads, 4 KV heads, MLP 10240)
+    of int4 group-128 weights: RMSNorm->QKV, attention replaced by a copy of
+    [M, 4096], o_proj + residual, RMSNorm->gate|up SiLU-gate, down + residual;
+    then a final RMSNorm -> bf16 head K2560 N8192.  One HIP graph per step."""
+    H, QKV, ATT, MLP, LAYERS, VOCAB, M = 2560, 6144, 4096, 10240, 26, 8192, 1
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+
+    def q4(n, k):
+        w = torch.randn(n, k, device=dev, generator=gen) * 0.02
+        p, sz, _ = G.quantize_int4_device(w, GROUP, True, G.W_INT4_ZP)
+        return p, sz
+
+    def gam(k):
+        return (1 + 0.1 * torch.randn(k, device=dev, generator=gen)).to(torch.bfloat16)
+
+    layers = [dict(qkv=q4(QKV, H), o=q4(H, ATT), gu=q4(2 * MLP, H), dn=q4(H, MLP), g1=gam(H), g2=gam(H))
+              for _ in range(LAYERS)]
+    head = (torch.randn(VOCAB, H, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+    gf = gam(H)
+    h0 = torch.randn(M, H, device=dev, generator=gen).to(torch.bfloat16)
+    hs = torch.empty_like(h0)
+    qkv = torch.empty(M, QKV, device=dev, dtype=torch.bfloat16)
+    att = torch.empty(M, ATT, device=dev, dtype=torch.bfloat16)
+    mid = torch.empty(M, MLP, device=dev, dtype=torch.bfloat16)
+    logits = torch.empty(M, VOCAB, device=dev, dtype=torch.bfloat16)
+
+    def run():
+        hs.copy_(h0)
+        for L in layers:
+            G.gemv(hs, L["qkv"][0], G.W_INT4_ZP, QKV, sc0=L["qkv"][1], group=GROUP, gamma=L["g1"], eps=EPS, out=qkv)
+            att.copy_(qkv[:, :ATT])
+            G.gemv(att, L["o"][0], G.W_INT4_ZP, H, sc0=L["o"][1], group=GROUP, epilogue=G.EPI_RESIDUAL,
+                   residual=hs, out=hs)
+            G.gemv(hs, L["gu"][0], G.W_INT4_ZP, 2 * MLP, sc0=L["gu"][1], group=GROUP, gamma=L["g2"], eps=EPS,
+                   epilogue=G.EPI_SILU_GATE, out=mid)
+            G.gemv(mid, L["dn"][0], G.W_INT4_ZP, H, sc0=L["dn"][1], group=GROUP, epilogue=G.EPI_RESIDUAL,
+                   residual=hs, out=hs)
+        G.gemv(hs, head, G.W_BF16, VOCAB, gamma=gf, eps=EPS, out=logits)
+
+    nbytes = LAYERS * (algo_bytes(4, QKV, H, M, True, 0) + 2 * 2 * M * ATT + algo_bytes(4, H, ATT, M, False, 2)
+                       + algo_bytes(4, 2 * MLP, H, M, True, 1) + algo_bytes(4, H, MLP, M, False, 2)) \
+        + algo_bytes(16, VOCAB, H, M, True, 0)
+    run()
+    torch.cuda.synchronize()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(st):
+        with torch.cuda.graph(g, stream=st):
+            run()
+    torch.cuda.current_stream().wait_stream(st)
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    reps = 20
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_ev.record()
+    for _ in range(reps):
+        g.replay()
+    e_ev.record()
+    torch.cuda.synchronize()
+    us = s_ev.elapsed_time(e_ev) * 1e3 / reps
+    roof = nbytes / HBM_PEAK_GBPS / 1e3
+    log(f"decode step (26 layers + head, M=1): {us:.1f} us, roofline {roof:.1f} us ({us / roof:.2f}x)")
+    del g, layers, head
+    torch.cuda.empty_cache()
+    return {"us": round(us, 2), "algorithmic_bytes": nbytes, "roofline_us": round(roof, 2),
+            "x_roofline": round(us / roof, 3), "M": M}
+
+
+if __name__ == "__main__":
+    sys.exit(main())
