@@ -21,6 +21,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
+from ._swap import swap_linears
 from .gemv import W_FP8, gemv_traceable, quantize_fp8_device
 
 # Max representable magnitude of float8_e4m3fn.
@@ -78,27 +79,19 @@ def quantize_module_fp8(
     min_bytes: int = MIN_QUANT_BYTES,
 ) -> dict[str, int]:
     """Swap qualifying Linear layers under ``root`` for FP8 equivalents
-    (models/fp8_linear.py:89-122)."""
-    converted = 0
-    saved_bytes = 0
-    skipped_small = 0
-
-    for module in root.modules():
-        for child_name, child in list(module.named_children()):
-            if not isinstance(child, nn.Linear) or child.bias is not None:
-                continue
-            if target_names and child_name not in target_names:
-                continue
-            nbytes = child.weight.numel() * child.weight.element_size()
-            if nbytes < min_bytes:
-                skipped_small += 1
-                continue
-            setattr(module, child_name, Fp8Linear(child))
-            converted += 1
-            saved_bytes += nbytes // 2
-
+    (models/fp8_linear.py:89-122).  Construction errors propagate, as in the
+    reference.  Saved bytes: fp8 keeps half of a bf16 weight."""
+    st = swap_linears(
+        root,
+        target_names,
+        min_bytes,
+        build=Fp8Linear,
+        saved_bytes=lambda nbytes: nbytes // 2,
+        tolerate_errors=False,
+        drop_original=False,
+    )
     return {
-        "converted": converted,
-        "skipped_below_threshold": skipped_small,
-        "weight_bytes_saved": saved_bytes,
+        "converted": st.converted,
+        "skipped_below_threshold": st.small,
+        "weight_bytes_saved": st.saved,
     }

@@ -28,6 +28,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
+from ._swap import swap_linears
 from .gemv import W_INT4_ZP, gemv_traceable, quantize_int4_device
 
 GROUP_SIZE = 128
@@ -80,20 +81,14 @@ class Int4Linear(nn.Module):
         super().__init__()
         if linear.bias is not None:
             raise ValueError("Int4Linear expects a bias-free Linear")
-
-        weight = linear.weight.data
-        if device is not None:
-            weight = weight.to(device)
-        self.out_features = int(weight.shape[0])
-        self.in_features = int(weight.shape[1])
+        # A CPU-resident model can be quantized one layer at a time on the GPU
+        # by passing device=; only the packed form stays.
+        weight = linear.weight.data if device is None else linear.weight.data.to(device)
+        self.out_features, self.in_features = (int(d) for d in weight.shape)
         self.group_size = group_size
-        if self.in_features % group_size:
-            raise ValueError(
-                f"in_features {self.in_features} not divisible by group {group_size}"
-            )
-
-        inner, scales_zeros = quantize_int4(weight, group_size)
-        self.register_buffer("weight_int4", inner)
+        _check_group(self.in_features, group_size)
+        packed, scales_zeros = quantize_int4(weight, group_size)
+        self.register_buffer("weight_int4", packed)
         self.register_buffer("scales_zeros", scales_zeros)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -126,35 +121,21 @@ def quantize_module_int4(
 ) -> dict[str, int]:
     """Swap qualifying Linear layers under ``root`` for int4 equivalents
     (models/int4_linear.py:118-164).  A layer that cannot be packed is left
-    untouched and counted as ``skipped_unsupported``."""
-    converted = 0
-    saved_bytes = 0
-    skipped_small = 0
-    skipped_unsupported = 0
-
-    for module in root.modules():
-        for child_name, child in list(module.named_children()):
-            if not isinstance(child, nn.Linear) or child.bias is not None:
-                continue
-            if target_names and child_name not in target_names:
-                continue
-            nbytes = child.weight.numel() * child.weight.element_size()
-            if nbytes < min_bytes:
-                skipped_small += 1
-                continue
-            try:
-                replacement = Int4Linear(child, group_size=group_size, device=device)
-            except Exception:  # noqa: BLE001 - shape/geometry rejections
-                skipped_unsupported += 1
-                continue
-            setattr(module, child_name, replacement)
-            child.weight = None
-            converted += 1
-            saved_bytes += nbytes - nbytes // 4
-
+    untouched and counted as ``skipped_unsupported``; the bf16 original of a
+    converted layer is released at once.  Saved bytes: int4 keeps a quarter
+    of a bf16 weight."""
+    st = swap_linears(
+        root,
+        target_names,
+        min_bytes,
+        build=lambda lin: Int4Linear(lin, group_size=group_size, device=device),
+        saved_bytes=lambda nbytes: nbytes - nbytes // 4,
+        tolerate_errors=True,
+        drop_original=True,
+    )
     return {
-        "converted": converted,
-        "skipped_below_threshold": skipped_small,
-        "skipped_unsupported": skipped_unsupported,
-        "weight_bytes_saved": saved_bytes,
+        "converted": st.converted,
+        "skipped_below_threshold": st.small,
+        "skipped_unsupported": st.unsupported,
+        "weight_bytes_saved": st.saved,
     }

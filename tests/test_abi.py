@@ -1,0 +1,168 @@
+"""The C ABI of libbzgemv.so without a GPU: the library loads, exports every
+function include/bz_gemv.h declares, the ctypes descriptor matches the C
+struct byte for byte, and argument validation answers with the documented
+status codes before anything touches a device."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "bz_gemv.h"
+
+
+@pytest.fixture(scope="module")
+def L():
+    from breeze_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        from breeze_amd import build
+
+        build.build()
+    return _lib
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(bz_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_exports(L):
+    assert declared_functions() == sorted(L.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(L):
+    lib = L.lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    nm = shutil.which("nm")
+    if nm:
+        out = subprocess.run([nm, "-D", "--defined-only", str(L.LIB_PATH)], capture_output=True, text=True).stdout
+        syms = {line.split()[-1] for line in out.splitlines() if line.strip()}
+        for name in declared_functions():
+            assert name in syms, name
+
+
+def test_abi_version_matches_header(L):
+    v = int(re.search(r"#define\s+BZ_ABI_VERSION\s+(\d+)", HEADER.read_text()).group(1))
+    assert L.lib().bz_abi_version() == v == L.ABI_VERSION
+
+
+def test_enum_values_match_header(L):
+    pairs = re.findall(r"\b(BZ_[A-Z0-9_]+)\s*=\s*(\d+)", HEADER.read_text())
+    assert len(pairs) >= 16
+    for name, val in pairs:
+        assert getattr(L, name[3:]) == int(val), name
+
+
+def test_strerror(L):
+    lib = L.lib()
+    msgs = [lib.bz_strerror(i).decode() for i in range(7)]
+    assert msgs[0] == "ok" and len(set(msgs)) == 7
+    assert lib.bz_strerror(99).decode() == "unknown status"
+
+
+def test_descriptor_layout_matches_c(L, tmp_path):
+    gcc = shutil.which("gcc")
+    if not gcc:
+        pytest.skip("gcc not available")
+    fields = [f for f, _ in L.GemvDesc._fields_]
+    src = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void) {",
+           '  printf("size %zu\\n", sizeof(bz_gemv_desc));']
+    src += [f'  printf("{f} %zu\\n", offsetof(bz_gemv_desc, {f}));' for f in fields]
+    src += ["  return 0;", "}"]
+    c = tmp_path / "layout.c"
+    c.write_text("\n".join(src))
+    exe = tmp_path / "layout"
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Werror", str(c), "-o", str(exe)], check=True)
+    got = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True).stdout.splitlines())
+    assert int(got["size"]) == ctypes.sizeof(L.GemvDesc)
+    for f in fields:
+        assert int(got[f]) == getattr(L.GemvDesc, f).offset, f
+
+
+def _desc(L, **kw):
+    d = L.GemvDesc()
+    d.abi_version = L.ABI_VERSION
+    d.M, d.N, d.K, d.group = 1, 64, 256, 128
+    d.wfmt, d.epilogue, d.out_dtype = L.W_INT4_ZP, L.EPI_NONE, L.DT_BF16
+    d.eps = 1e-6
+    fake = 1 << 20  # never dereferenced: every case below fails validation
+    d.x, d.ldx, d.w, d.sc0, d.out, d.ldo = fake, 256, fake, fake, fake, 64
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+@pytest.mark.parametrize(
+    "kw,status",
+    [
+        ({"abi_version": 99}, "ERR_ABI"),
+        ({"M": 0}, "ERR_INVALID_ARG"),
+        ({"wfmt": 7}, "ERR_INVALID_ARG"),
+        ({"epilogue": 5}, "ERR_INVALID_ARG"),
+        ({"out_dtype": 3}, "ERR_INVALID_ARG"),
+        ({"x": None}, "ERR_INVALID_ARG"),
+        ({"sc0": None}, "ERR_INVALID_ARG"),
+        ({"wfmt": 1}, "ERR_INVALID_ARG"),                      # INT4_MIN needs sc1
+        ({"epilogue": 2}, "ERR_INVALID_ARG"),                  # RESIDUAL needs residual
+        ({"K": 200}, "ERR_SHAPE"),                             # K % group
+        ({"group": 96}, "ERR_SHAPE"),                          # not a power of two
+        ({"group": 16, "K": 256}, "ERR_SHAPE"),                # below 32
+        ({"epilogue": 1, "N": 63}, "ERR_SHAPE"),               # SiLU-gate needs even N
+        ({"wfmt": 2, "K": 264}, "ERR_SHAPE"),                  # fp8 K % 16
+        ({"wfmt": 3, "K": 260}, "ERR_SHAPE"),                  # bf16 K % 8
+        ({"ldx": 100}, "ERR_INVALID_ARG"),                     # ldx < K
+        ({"x": (1 << 20) + 2}, "ERR_ALIGNMENT"),
+        ({"w": (1 << 20) + 8}, "ERR_ALIGNMENT"),
+        ({"ldx": 260}, "ERR_ALIGNMENT"),                       # rows not 16-byte aligned
+        ({"cfg_path": 3}, "ERR_INVALID_ARG"),
+        ({"cfg_depth": 3}, "ERR_INVALID_ARG"),
+        ({"cfg_depth": 16, "epilogue": 1}, "ERR_INVALID_ARG"),  # 2 x 16 loads in flight
+        ({"cfg_waves": 9}, "ERR_INVALID_ARG"),
+        ({"group": 64, "cfg_path": 2}, "ERR_UNSUPPORTED"),      # MFMA path needs group >= 128
+    ],
+)
+def test_gemv_validation(L, kw, status):
+    d = _desc(L, **kw)
+    assert L.lib().bz_gemv(ctypes.byref(d), None) == getattr(L, status)
+
+
+def test_gemv_null_descriptor(L):
+    assert L.lib().bz_gemv(None, None) == L.ERR_INVALID_ARG
+
+
+def test_workspace_is_zero(L):
+    d = _desc(L)
+    assert L.lib().bz_gemv_workspace(ctypes.byref(d)) == 0
+
+
+def test_aux_validation(L):
+    lib = L.lib()
+    f = 1 << 20
+    assert lib.bz_rmsnorm(None, 8, f, 1e-6, f, 8, 1, 8, None) == L.ERR_INVALID_ARG
+    assert lib.bz_rmsnorm(f, 4, f, 1e-6, f, 8, 1, 8, None) == L.ERR_INVALID_ARG
+    assert lib.bz_silu_mul(f, 8, f, 8, f, 8, 0, 8, None) == L.ERR_INVALID_ARG
+    assert lib.bz_quantize_int4(f, 1, 8, 256, 96, 0, 0, f, f, None, None) == L.ERR_SHAPE
+    assert lib.bz_quantize_int4(f, 1, 8, 256, 128, 0, 1, f, f, None, None) == L.ERR_INVALID_ARG
+    assert lib.bz_quantize_int4(f, 5, 8, 256, 128, 0, 0, f, f, None, None) == L.ERR_INVALID_ARG
+    assert lib.bz_quantize_fp8(f, 5, 8, 256, 1e-12, f, f, None) == L.ERR_INVALID_ARG
+    assert lib.bz_dequant(0, f, f, None, 8, 200, 128, f, None) == L.ERR_SHAPE
+    assert lib.bz_dequant(0, f + 4, f, None, 8, 256, 128, f, None) == L.ERR_ALIGNMENT
+    assert lib.bz_dequant(9, f, f, None, 8, 256, 128, f, None) == L.ERR_INVALID_ARG
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    from breeze_amd import _lib
+
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "absent.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(RuntimeError, match="no fallback"):
+        _lib.lib()

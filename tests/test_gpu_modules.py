@@ -1,0 +1,326 @@
+"""GPU tests of the reference-shaped modules and of the committed golden
+fixtures, all through the C ABI (libbzgemv.so).
+
+Bars: bit-exact for quantizer outputs, packing and dequantized weights;
+max|out-ref|/max|ref| <= 1e-2 for GEMV outputs against the CPU oracle's
+float64 product on the fp32 RMSNorm (the reference's own definition,
+bench_gemv.py:30-53)."""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from oracle import bz_oracle as O
+from tests._util import bf16_bits, bf16_tensor, f32, u8_tensor
+
+from breeze_amd import fp8_linear as F8
+from breeze_amd import gemv as G
+from breeze_amd import int4_linear as I4
+from breeze_amd.fused import kernels as FK
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+TOL = 1e-2
+
+
+def _dev():
+    return torch.device("cuda", 0)
+
+
+# ---------------------------------------------------------------------------
+# golden fixtures
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("name", ["int4_asym_g128", "int4_sym_g128", "int4_asym_g32"])
+def test_golden_int4(name):
+    f = np.load(GOLDEN / f"{name}.npz")
+    n, k, m, group, sym = (int(v) for v in f["meta"])
+    # quantizer: bit-exact packed bytes and scales_zeros
+    packed, sz, _ = G.quantize_int4_device(torch.from_numpy(f["w"]).to(_dev()), group, bool(sym), G.W_INT4_ZP)
+    assert np.array_equal(packed.cpu().numpy(), f["packed_even_low"])
+    assert np.array_equal(bf16_bits(sz), f["scales_zeros"])
+    if not sym:
+        p2, s2, m2 = G.quantize_int4_device(torch.from_numpy(f["w"]).to(_dev()), group, False, G.W_INT4_MIN)
+        assert np.array_equal(p2.cpu().numpy(), f["packed_even_low"])
+        assert np.array_equal(bf16_bits(s2), f["scale_bits"]) and np.array_equal(bf16_bits(m2), f["min_bits"])
+    # dequant: bit-exact in both scale layouts
+    d_p = u8_tensor(f["packed_even_low"])
+    got = G.dequant(G.W_INT4_ZP, d_p, n, k, sc0=bf16_tensor(f["scales_zeros"]), group=group)
+    assert np.array_equal(got.cpu().numpy(), f["w_eff_zp"])
+    got = G.dequant(G.W_INT4_MIN, d_p, n, k, sc0=bf16_tensor(f["scale_bits"]), sc1=bf16_tensor(f["min_bits"]),
+                    group=group)
+    assert np.array_equal(got.cpu().numpy(), f["w_eff_min"])
+    # GEMVs against the stored float64 references
+    x, g = bf16_tensor(f["x"]), bf16_tensor(f["gamma"])
+    sz_d = bf16_tensor(f["scales_zeros"])
+    for path in (1, 2):
+        if path == 2 and group < 128:
+            continue
+        cfg = (0, 0, 0, path)
+        out = G.gemv(x, d_p, G.W_INT4_ZP, n, sc0=sz_d, group=group, gamma=g, out_dtype=torch.float32, cfg=cfg)
+        assert O.rel_err(f32(out), f["out_norm_none"]) <= TOL
+        out = G.gemv(x, d_p, G.W_INT4_ZP, n, sc0=sz_d, group=group, gamma=g, epilogue=G.EPI_SILU_GATE, cfg=cfg)
+        assert O.rel_err(f32(out), f["out_norm_silu"]) <= TOL
+        out = G.gemv(x, d_p, G.W_INT4_ZP, n, sc0=sz_d, group=group, epilogue=G.EPI_RESIDUAL,
+                     residual=bf16_tensor(f["residual"]), cfg=cfg)
+        assert O.rel_err(f32(out), f["out_plain_res"]) <= TOL
+        out = G.gemv(x, d_p, G.W_INT4_MIN, n, sc0=bf16_tensor(f["scale_bits"]), sc1=bf16_tensor(f["min_bits"]),
+                     group=group, cfg=cfg)
+        assert O.rel_err(f32(out), f["out_min_none"]) <= TOL
+
+
+def test_golden_fp8():
+    f = np.load(GOLDEN / "fp8_row.npz")
+    n, k, m = (int(v) for v in f["meta"])
+    w = torch.from_numpy(f["w"]).to(_dev())
+    codes, scale = G.quantize_fp8_device(w, 1e-12)
+    assert np.array_equal(codes.view(torch.uint8).cpu().numpy(), f["codes"])
+    assert np.array_equal(scale.cpu().numpy(), f["scale"])
+    c8, s8 = G.quantize_fp8_device(w, 1e-8)
+    assert np.array_equal(c8.view(torch.uint8).cpu().numpy(), f["codes_fused"])
+    assert np.array_equal(s8.cpu().numpy(), f["scale_fused"])
+    d_c = u8_tensor(f["codes"])
+    d_s = torch.from_numpy(f["scale"]).to(_dev())
+    # decoded codes times the row scale is bit-exact
+    got = G.dequant(G.W_FP8, d_c, n, k, sc0=d_s)
+    assert np.array_equal(got.cpu().numpy(), f["w_eff"])
+    x, g = bf16_tensor(f["x"]), bf16_tensor(f["gamma"])
+    for path in (1, 2):
+        out = G.gemv(x, d_c, G.W_FP8, n, sc0=d_s, gamma=g, out_dtype=torch.float32, cfg=(0, 0, 0, path))
+        assert O.rel_err(f32(out), f["out_norm_none"]) <= TOL
+        out = G.gemv(x, d_c, G.W_FP8, n, sc0=d_s, epilogue=G.EPI_SILU_GATE, cfg=(0, 0, 0, path))
+        assert O.rel_err(f32(out), f["out_plain_silu"]) <= TOL
+
+
+# ---------------------------------------------------------------------------
+# Int4Linear / Fp8Linear (models/int4_linear.py:67-115, models/fp8_linear.py:44-86)
+# ---------------------------------------------------------------------------
+
+
+def _linear(n, k, seed, device):
+    w, _, _ = O.synth(n, k, 1, seed=seed)
+    lin = nn.Linear(k, n, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(torch.from_numpy(w))
+    return lin.to(device), w
+
+
+@pytest.mark.parametrize("device", ["cuda", "cpu"])
+def test_int4_linear_buffers_and_forward(device):
+    N, K = 384, 1024
+    lin, w = _linear(N, K, 20, device)
+    mod = I4.Int4Linear(lin, device="cuda" if device == "cpu" else None)
+    assert mod.in_features == K and mod.out_features == N and mod.group_size == 128
+    assert mod.weight_int4.dtype == torch.int32 and tuple(mod.weight_int4.shape) == (N, K // 8)
+    assert mod.scales_zeros.dtype == torch.bfloat16 and tuple(mod.scales_zeros.shape) == (K // 128, N, 2)
+    q, s, lo, z = O.quantize_int4_asym(w, 128)
+    assert np.array_equal(mod.weight_int4.cpu().view(torch.uint8).numpy(), O.pack_nibbles_even_low(q))
+    sz = O.scales_zeros(s, z)
+    assert np.array_equal(bf16_bits(mod.scales_zeros), sz)
+    w_eff = O.dequant_int4_zp(q, sz, 128)
+    for shape, dtype in (((1, K), torch.bfloat16), ((2, 3, K), torch.bfloat16), ((5, K), torch.float32)):
+        x = torch.randn(*shape, generator=torch.Generator().manual_seed(3)).to(dtype)
+        y = mod(x.to(_dev()))
+        assert y.dtype == dtype and tuple(y.shape) == shape[:-1] + (N,)
+        xr = x.to(torch.bfloat16).float().reshape(-1, K).numpy()
+        assert O.rel_err(f32(y).reshape(-1, N), O.gemv_ref(xr, w_eff)) <= TOL
+
+
+def test_int4_linear_rebuilt_from_buffers():
+    """The quantized-checkpoint loader builds modules with __new__ +
+    nn.Module.__init__ + attributes + register_buffer
+    (models/quantized_checkpoint.py:91-107); forward must need nothing else."""
+    N, K = 256, 512
+    lin, w = _linear(N, K, 21, "cuda")
+    ref = I4.Int4Linear(lin)
+    mod = I4.Int4Linear.__new__(I4.Int4Linear)
+    nn.Module.__init__(mod)
+    mod.in_features, mod.out_features, mod.group_size = K, N, 128
+    mod.register_buffer("weight_int4", ref.weight_int4.clone())
+    mod.register_buffer("scales_zeros", ref.scales_zeros.clone())
+    x = torch.randn(2, K, device=_dev()).to(torch.bfloat16)
+    assert torch.equal(mod(x), ref(x))
+
+
+def test_fp8_linear_buffers_and_forward():
+    N, K = 320, 768
+    lin, w = _linear(N, K, 22, "cuda")
+    mod = F8.Fp8Linear(lin)
+    assert mod.weight_fp8.dtype == torch.float8_e4m3fn and tuple(mod.weight_fp8.shape) == (N, K)
+    assert mod.weight_scale.dtype == torch.float32 and tuple(mod.weight_scale.shape) == (1, N)
+    codes, scale = O.quantize_fp8_linear(w)
+    assert np.array_equal(mod.weight_fp8.view(torch.uint8).cpu().numpy(), codes)
+    assert np.array_equal(mod.weight_scale.cpu().numpy()[0], scale)
+    x = torch.randn(3, K, device=_dev()).to(torch.bfloat16)
+    y = mod(x)
+    assert y.dtype == torch.bfloat16 and tuple(y.shape) == (3, N)
+    ref = O.gemv_ref(x.float().cpu().numpy(), O.dequant_fp8(codes, scale))
+    assert O.rel_err(f32(y), ref) <= TOL
+
+
+class _Mlp(nn.Module):
+    def __init__(self, k, n):
+        super().__init__()
+        self.gate_proj = nn.Linear(k, n, bias=False)
+        self.up_proj = nn.Linear(k, n, bias=False)
+        self.down_proj = nn.Linear(n, k, bias=False)
+
+    def forward(self, x):
+        return self.down_proj(torch.nn.functional.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+def test_quantize_module_int4_converts_large_layers():
+    torch.manual_seed(0)
+    m = _Mlp(2048, 1536).to(_dev())          # 12 MB fp32 each: above the 8 MB threshold
+    for p in m.parameters():
+        nn.init.normal_(p, std=0.02)
+    x = torch.randn(2, 2048, device=_dev())
+    want = m(x)
+    nbytes = 2048 * 1536 * 4
+    stats = I4.quantize_module_int4(m)
+    assert stats == {"converted": 3, "skipped_below_threshold": 0, "skipped_unsupported": 0,
+                     "weight_bytes_saved": 3 * (nbytes - nbytes // 4)}
+    assert all(type(getattr(m, n)) is I4.Int4Linear for n in ("gate_proj", "up_proj", "down_proj"))
+    got = m(x)
+    assert got.dtype == torch.float32
+    # against the same MLP on the dequantized weights (decode pinned bit-exact
+    # by the golden tests), fp32: only the kernel's bf16 activations differ
+    wd = {n: G.dequant(G.W_INT4_ZP, getattr(m, n).weight_int4, getattr(m, n).out_features,
+                       getattr(m, n).in_features, sc0=getattr(m, n).scales_zeros)
+          for n in ("gate_proj", "up_proj", "down_proj")}
+    h = torch.nn.functional.silu(x @ wd["gate_proj"].t()) * (x @ wd["up_proj"].t())
+    assert O.rel_err(f32(got), f32(h @ wd["down_proj"].t())) <= TOL
+    # and the quantization error itself stays at int4 group-128 level
+    assert O.rel_err(f32(got), f32(want)) <= 0.35
+
+
+def test_quantize_module_fp8_converts_large_layers():
+    torch.manual_seed(1)
+    m = _Mlp(2048, 1536).to(_dev())
+    for p in m.parameters():
+        nn.init.normal_(p, std=0.02)
+    x = torch.randn(2, 2048, device=_dev())
+    want = m(x)
+    stats = F8.quantize_module_fp8(m)
+    nbytes = 2048 * 1536 * 4
+    assert stats == {"converted": 3, "skipped_below_threshold": 0, "weight_bytes_saved": 3 * (nbytes // 2)}
+    got = m(x)
+    wd = {n: G.dequant(G.W_FP8, getattr(m, n).weight_fp8.view(torch.uint8), getattr(m, n).out_features,
+                       getattr(m, n).in_features, sc0=getattr(m, n).weight_scale)
+          for n in ("gate_proj", "up_proj", "down_proj")}
+    h = torch.nn.functional.silu(x @ wd["gate_proj"].t()) * (x @ wd["up_proj"].t())
+    assert O.rel_err(f32(got), f32(h @ wd["down_proj"].t())) <= TOL
+    assert O.rel_err(f32(got), f32(want)) <= 0.1
+
+
+# ---------------------------------------------------------------------------
+# fused/ host API (models/fused/kernels.py, models/fused/layer.py)
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("bits", [4, 8, 16])
+@pytest.mark.parametrize("epi", [0, 1, 2])
+def test_rms_gemv(bits, epi):
+    N, K, M = 512, 1024, 2
+    w, gamma, x = O.synth(N, K, M, seed=30 + bits + epi)
+    fw = FK.FusedWeight(torch.from_numpy(w).to(_dev()), bits=bits)
+    xd, gd = bf16_tensor(x), bf16_tensor(gamma)
+    n_out = N // 2 if epi == 1 else N
+    res = torch.randn(M, n_out, device=_dev()).to(torch.bfloat16) if epi == 2 else None
+    out = FK.rms_gemv(xd, fw, gd, 1e-6, epilogue=epi, residual=res)
+    if bits == 4:
+        q = O.unpack_nibbles_even_low(fw.w.cpu().numpy())
+        w_eff = O.dequant_int4_min(q, bf16_bits(fw.s), bf16_bits(fw.z), 128)
+        packed, s_bits, m_bits = O.pack_int4_fused(w)
+        assert np.array_equal(fw.w.cpu().numpy(), packed)           # pack_int4 bit-exact
+        assert np.array_equal(bf16_bits(fw.s), s_bits) and np.array_equal(bf16_bits(fw.z), m_bits)
+    elif bits == 8:
+        codes, scale = O.pack_fp8(w)
+        assert np.array_equal(fw.w.view(torch.uint8).cpu().numpy(), codes)
+        assert np.array_equal(fw.s.cpu().numpy(), scale)
+        w_eff = O.dequant_fp8(codes, scale)
+    else:
+        w_eff = O.round_bf16(w)
+    xn = O.rmsnorm_f32(O.bf16_bits_to_f32(x), O.bf16_bits_to_f32(gamma))
+    ref = O.gemv_ref(xn, w_eff, epi, res.float().cpu().numpy() if res is not None else None)
+    assert tuple(out.shape) == (M, n_out)
+    assert O.rel_err(f32(out), ref) <= TOL
+
+
+def test_from_int4_gate_up_silu():
+    """Two Int4Linear modules fused as [gate; up] with the SiLU-gate epilogue
+    (models/fused/layer.py:56-60, kernels.py:116-127)."""
+    K, H = 1024, 384
+    g_lin, wg = _linear(H, K, 40, "cuda")
+    u_lin, wu = _linear(H, K, 41, "cuda")
+    gm, um = I4.Int4Linear(g_lin), I4.Int4Linear(u_lin)
+    fw = FK.FusedWeight.from_int4(gm, um)
+    assert fw.N == 2 * H and fw.K == K and fw.layout == "zp"
+    _, gamma, x = O.synth(1, K, 2, seed=42)
+    out = FK.rms_gemv(bf16_tensor(x), fw, bf16_tensor(gamma), 1e-6, epilogue=FK.EPI_SILU_GATE)
+    xn = O.rmsnorm_f32(O.bf16_bits_to_f32(x), O.bf16_bits_to_f32(gamma))
+    qg, sg, _, zg = O.quantize_int4_asym(wg, 128)
+    qu, su, _, zu = O.quantize_int4_asym(wu, 128)
+    w_eff = np.concatenate([O.dequant_int4_zp(qg, O.scales_zeros(sg, zg)), O.dequant_int4_zp(qu, O.scales_zeros(su, zu))])
+    assert O.rel_err(f32(out), O.gemv_ref(xn, w_eff, O.EPI_SILU)) <= TOL
+
+
+def test_from_fp8_concat():
+    K = 768
+    mods = [F8.Fp8Linear(_linear(n, K, 50 + i, "cuda")[0]) for i, n in enumerate((256, 64, 64))]
+    fw = FK.FusedWeight.from_fp8(*mods)
+    assert fw.N == 384 and fw.s.shape == (384,)
+    x = torch.randn(1, K, device=_dev()).to(torch.bfloat16)
+    out = FK.rms_gemv(x, fw)
+    want = torch.cat([m(x) for m in mods], dim=1)
+    assert O.rel_err(f32(out), f32(want)) <= 1e-2
+
+
+def test_rmsnorm_and_silu_mul_kernels():
+    M, K = 3, 2560
+    _, gamma, x = O.synth(1, K, M, seed=60)
+    y = FK.rmsnorm(bf16_tensor(x), bf16_tensor(gamma), 1e-6)
+    ref = O.rmsnorm_f32(O.bf16_bits_to_f32(x), O.bf16_bits_to_f32(gamma))
+    assert np.all(np.abs(f32(y) - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-30)
+    g = torch.randn(M, 1000, device=_dev()).to(torch.bfloat16)
+    u = torch.randn(M, 1000, device=_dev()).to(torch.bfloat16)
+    got = f32(FK.silu_mul(g, u))
+    want = O.silu(f32(g)) * f32(u)
+    assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 1e-6)
+
+
+# ---------------------------------------------------------------------------
+# HIP graph capture: every replay equals the eager result
+# ---------------------------------------------------------------------------
+
+
+def test_graph_replays_match_eager():
+    N, K, M = 2048, 2560, 1
+    w, gamma, x = O.synth(N, K, M, seed=70)
+    fw = FK.FusedWeight(torch.from_numpy(w).to(_dev()), bits=4)
+    xd, gd = bf16_tensor(x), bf16_tensor(gamma)
+    out = torch.empty(M, N // 2, device=_dev(), dtype=torch.bfloat16)
+    eager = FK.rms_gemv(xd, fw, gd, 1e-6, epilogue=FK.EPI_SILU_GATE).clone()
+    args = fw.gemv_args()
+    wt, wf = args.pop("w"), args.pop("wfmt")
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(st):
+        with torch.cuda.graph(g, stream=st):
+            G.gemv(xd, wt, wf, N, gamma=gd, eps=1e-6, epilogue=G.EPI_SILU_GATE, out=out, **args)
+    torch.cuda.current_stream().wait_stream(st)
+    for i in range(4):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+        _ = (xd.float() * 2).sum().item()  # unrelated eager work between replays
