@@ -94,20 +94,22 @@ extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
     const int ntiles = (n_out + cols_per_tile - 1) / cols_per_tile;
     Launch l;
     l.silu = silu;
-    // Measured on MI355X: 8 waves x 2 steps in flight per wave stream the
-    // decode shapes best (deeper per-wave pipelines do not help once 8 waves
-    // share a CU); bf16 rows, with fewer k per byte, prefer 4 steps.
-    l.depth = d->cfg_depth ? d->cfg_depth : (wf == BZ_W_BF16 && T == 1 ? 4 : 2);
-    if ((l.depth != 2 && l.depth != 4 && l.depth != 8 && l.depth != 16) || l.depth * T > kMaxLoadsInFlight)
-        return BZ_ERR_INVALID_ARG;
-    const int max_waves = kMaxThreads / 64;
-    l.nw = d->cfg_waves ? d->cfg_waves : (nunits > max_waves ? max_waves : nunits);
-    if (l.nw < 1 || l.nw > max_waves) return BZ_ERR_INVALID_ARG;
+    l.nw = d->cfg_waves ? d->cfg_waves : (nunits > kMaxWaves ? kMaxWaves : nunits);
+    if (l.nw < 1 || l.nw > kMaxWaves) return BZ_ERR_INVALID_ARG;
     if (l.nw > nunits) l.nw = nunits;  // every wave owns at least one unit of each tile
     int tpw = d->cfg_tiles ? d->cfg_tiles : (ntiles + kTargetWorkgroups - 1) / kTargetWorkgroups;
     if (tpw < 1) return BZ_ERR_INVALID_ARG;
     if (tpw > ntiles) tpw = ntiles;
     l.grid = (unsigned)((ntiles + tpw - 1) / tpw);
+    if (d->cfg_depth && ((d->cfg_depth != 2 && d->cfg_depth != 4 && d->cfg_depth != 8 && d->cfg_depth != 16) ||
+                         d->cfg_depth * T > kMaxLoadsInFlight))
+        return BZ_ERR_INVALID_ARG;
+    // (argument validation ends here: the rest may query the device)
+    // Measured on MI355X: 8 waves x 2 steps in flight per wave stream the
+    // decode shapes best (deeper per-wave pipelines only lengthen the queue
+    // the x loads wait in); bf16 rows, with fewer k per byte, prefer 4 steps.
+    l.depth = d->cfg_depth ? d->cfg_depth : (wf == BZ_W_BF16 && T == 1 ? 4 : 2);
+    const int lds_lim = device_lds_limit();
     const int nchunks = (int)((row_bytes + 127) / 128);
 
     GemvParams p;
@@ -134,7 +136,6 @@ extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
     p.norm = d->gamma != nullptr;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const size_t osz = p.out_f32 ? 4 : 2, rsz = p.res_f32 ? 4 : 2;
-    const int lds_lim = device_lds_limit();
     for (int m0 = 0; m0 < M; m0 += kMaxRowsPerLaunch) {
         l.M = (M - m0) < kMaxRowsPerLaunch ? (M - m0) : kMaxRowsPerLaunch;
         const int lds = mfma ? mfma_lds_layout(l.M, T, l.nw, K, wf, tpw).total

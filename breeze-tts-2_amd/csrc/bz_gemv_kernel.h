@@ -20,11 +20,12 @@
 //     concatenation (models/fused/layer.py:60), so silu(g)*u needs no second
 //     pass.
 //   * The grid is persistent-sized (about one workgroup per CU).  Each
-//     workgroup owns `tpw` consecutive tiles; its NW waves split every tile's
-//     chunks round-robin (chunk ch -> wave ch % NW), so each wave walks
-//     tpw * cpw "steps" (one chunk of the T weight tiles each) through a
+//     workgroup owns `tpw` consecutive tiles, i.e. tpw * nchunks "steps"
+//     (one chunk of the T weight tiles each) in tile-major order; wave w
+//     takes steps w, w + NW, w + 2 NW, ... so every wave gets the same number
+//     of steps (+-1) whatever nchunks % NW is, and walks them through a
 //     rolling register pipeline that keeps D steps of loads in flight across
-//     tile boundaries.
+//     tile boundaries.  Nothing is loaded past a wave's last step.
 //   * x is staged once per workgroup into LDS.  Its loads are issued BEFORE
 //     the first weight loads: vector loads retire in issue order, so waiting
 //     for x does not wait for the (HBM-latency) weights.  The RMSNorm is
@@ -91,15 +92,20 @@ __host__ __device__ inline int x_row_elems(int K, int wf) {
 }
 
 // LDS carve-up, shared by the kernel and the host launcher.
+// Largest workgroup: 8 waves.
+constexpr int kMaxThreads = 512;
+constexpr int kMaxWaves = kMaxThreads / 64;
+
 struct LdsLayout {
     int xs, xsum, red, nrm, total;
 };
+// LDS: x, the int4 32-k sums of x, the parked partial sums, the norm.
 __host__ __device__ inline LdsLayout lds_layout(int M, int T, int NW, int K, int wf, int tpw) {
     const bool i4 = is_int4(wf);
     const int xe = x_row_elems(K, wf);
     LdsLayout L;
     L.xs = 0;
-    L.xsum = align16(M * xe * 2);
+    L.xsum = L.xs + align16(M * xe * 2);
     L.red = L.xsum + (i4 ? align16(M * (xe / 32) * 4) : 0);
     L.nrm = L.red + align16(tpw * NW * T * M * 8 * 4);
     L.total = L.nrm + align16(NW * M * 4);
@@ -126,9 +132,7 @@ __device__ __forceinline__ int x_block_addr(int kb) {
 // Blocks of x each thread keeps in registers during the prologue.
 constexpr int kXB = 4;
 
-// Largest workgroup: 8 waves.  A 512-thread bound lets a wave hold up to 256
-// VGPRs, room for 16 weight loads in flight.
-constexpr int kMaxThreads = 512;
+
 
 // Loads are unconditional (indices clamped into range) so the code stays
 // straight-line and the wait-count pass can wait for exactly the loads it
@@ -256,63 +260,217 @@ __device__ __forceinline__ float row_inv_rms(const GemvParams& p, const float* n
 }
 
 // ---------------------------------------------------------------------------
-// the streaming pipeline
+// epilogue (shared by the dot2 and MFMA kernels; COLS = output columns per
+// tile, which is also the row stride of the parked partial sums)
 // ---------------------------------------------------------------------------
 
-// Per-wave walk over its steps: local tile tl (outer) and chunk index jj
-// (inner; chunk ch = wave + jj * NW).  Both counters are wave-uniform.
-struct StepCursor {
-    int tl, jj;
-    __device__ __forceinline__ void advance(int cpw) {
-        if (++jj == cpw) {
-            jj = 0;
-            ++tl;
-        }
+// Output i of a workgroup: local tile i / (M*COLS), x row (i / COLS) % M,
+// column i % COLS of the tile.
+template <int M, int COLS>
+struct OutIndex {
+    int tl, m, c;
+    __device__ __forceinline__ OutIndex(int i, int tile0) {
+        tl = i / (M * COLS);
+        m = (i / COLS) % M;
+        c = (tile0 + tl) * COLS + (i % COLS);
     }
 };
 
-// Issue the T weight loads of the step at cursor c (clamped to the wave's
-// last step past the end, so every load is unconditional), and for int4 the
+// What the epilogue reads from global memory (fp8 row scales, the residual)
+// for the first output a thread owns, loaded during the prologue so the
+// epilogue does not start with a memory round trip.
+template <int T>
+struct EpiPrefetch {
+    float sc[T];
+    uint32_t res;  // raw bits (f32, or bf16 zero-extended): converted in the epilogue, so
+                   // the prologue never waits for this load
+};
+
+template <int WF, int M, int T, bool SILU, int COLS>
+__device__ __forceinline__ EpiPrefetch<T> epi_prefetch(const GemvParams& p, int tile0, int ntl, int tid) {
+    const OutIndex<M, COLS> o(min(tid, ntl * M * COLS - 1), tile0);
+    const int c = min(o.c, p.n_out - 1);
+    EpiPrefetch<T> e;
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+        e.sc[t] = WF == WF_FP8 ? reinterpret_cast<const float*>(p.sc0)[SILU ? c + t * p.n_out : c] : 1.0f;
+    e.res = 0u;
+    if (p.epi == BZ_EPI_RESIDUAL) {
+        const int64_t idx = (int64_t)o.m * p.ldr + c;
+        e.res = p.res_f32 ? reinterpret_cast<const uint32_t*>(p.res)[idx]
+                          : (uint32_t)reinterpret_cast<const uint16_t*>(p.res)[idx];
+    }
+    return e;
+}
+
+// Sum the waves' parked partials of each output in a fixed order
+// (deterministic), apply 1/rms, the fp8 row scale, SiLU-gate or residual,
+// and store.  red[((tl*NW + w)*T + t)*M + m][COLS].
+template <int WF, int M, int T, bool SILU, int COLS>
+__device__ __forceinline__ void epilogue(const GemvParams& p, int tile0, int ntl, int tid, int nthr, int NW,
+                                         const float* red, const float* nrm, const EpiPrefetch<T>& pre) {
+    float inv[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) inv[m] = row_inv_rms(p, nrm, NW, M, m);
+    for (int i = tid; i < ntl * M * COLS; i += nthr) {
+        const OutIndex<M, COLS> o(i, tile0);
+        if (o.c >= p.n_out) continue;
+        const bool first = i == tid;
+        float iv = inv[0];
+#pragma unroll
+        for (int m = 1; m < M; ++m)
+            if (o.m == m) iv = inv[m];
+        float a[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            float v = 0.0f;
+            const float* rp = red + (((o.tl * NW) * T + t) * M + o.m) * COLS + (i % COLS);
+            for (int w = 0; w < NW; ++w) v += rp[w * T * M * COLS];
+            v *= iv;
+            if (WF == WF_FP8)
+                v *= first ? pre.sc[t] : reinterpret_cast<const float*>(p.sc0)[SILU ? o.c + t * p.n_out : o.c];
+            a[t] = v;
+        }
+        float out = SILU ? silu(a[0]) * a[T - 1] : a[0];
+        if (p.epi == BZ_EPI_RESIDUAL) {
+            const int64_t idx = (int64_t)o.m * p.ldr + o.c;
+            out += first ? __uint_as_float(p.res_f32 ? pre.res : pre.res << 16)
+                         : (p.res_f32 ? reinterpret_cast<const float*>(p.res)[idx]
+                                      : bf16_to_f32(reinterpret_cast<const uint16_t*>(p.res)[idx]));
+        }
+        const int64_t oi = (int64_t)o.m * p.ldo + o.c;
+        if (p.out_f32)
+            reinterpret_cast<float*>(p.out)[oi] = out;
+        else
+            reinterpret_cast<uint16_t*>(p.out)[oi] = f32_to_bf16(out);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// the streaming pipeline
+// ---------------------------------------------------------------------------
+
+// Position of a wave in the workgroup's tile-major step list: local tile tl
+// and chunk ch.  A wave advances by NW steps; NW <= nchunks (host-checked),
+// so a wave visits every tile, and its last step in a tile is the one with
+// ch + NW >= nchunks.  Both fields are wave-uniform.
+struct StepCursor {
+    int tl, ch;
+    __device__ __forceinline__ void advance(int NW, int nch) {
+        ch += NW;
+        if (ch >= nch) {
+            ch -= nch;
+            ++tl;
+        }
+    }
+    __device__ __forceinline__ bool last_in_tile(int NW, int nch) const { return ch + NW >= nch; }
+};
+
+// Steps of wave `wave` among ntl * nch, and the cursor of its last one.
+__device__ __forceinline__ int wave_steps(int ntl, int nch, int NW, int wave) {
+    return (ntl * nch - 1 - wave) / NW + 1;
+}
+__device__ __forceinline__ StepCursor step_cursor(int s, int NW, int nch, int wave) {
+    const int flat = wave + s * NW;
+    const int tl = flat / nch;
+    return StepCursor{tl, flat - tl * nch};
+}
+
+// The rolling pipeline shared by both kernels.  issue(d, c) loads step c
+// into register slot d; consume(d, c) uses slot d.  pipeline_prime issues the
+// first D steps (past the last step it re-issues the last one, so the
+// prologue stays branch-free); pipeline_run then consumes every step exactly
+// once and issues nothing past a wave's last step.  The steady loop issues
+// unconditionally, which keeps the compiler's vector-memory wait counts
+// exact (each consume waits only for its own slot); the tail issues behind a
+// wave-uniform branch.
+template <int D, typename IssueFn>
+__device__ __forceinline__ void pipeline_prime(int S, int NW, int nch, int wave, StepCursor& ic, IssueFn issue) {
+    const StepCursor last = step_cursor(S - 1, NW, nch, wave);
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        issue(d, d < S ? ic : last);
+        ic.advance(NW, nch);
+    }
+}
+
+template <int D, typename IssueFn, typename ConsumeFn>
+__device__ __forceinline__ void pipeline_run(int S, int NW, int nch, int wave, StepCursor ic, IssueFn issue,
+                                             ConsumeFn consume) {
+    StepCursor cc{0, wave};
+    int s0 = 0;
+    for (; s0 + 2 * D <= S; s0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            consume(d, cc);
+            cc.advance(NW, nch);
+            issue(d, ic);
+            ic.advance(NW, nch);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        const int s = s0 + d;
+        if (s < S) {
+            consume(d, cc);
+            cc.advance(NW, nch);
+        }
+        if (s + D < S) {
+            issue(d, ic);
+            ic.advance(NW, nch);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        const int s = s0 + D + d;
+        if (s < S) {
+            consume(d, cc);
+            cc.advance(NW, nch);
+        }
+    }
+}
+
+// Issue the T weight loads of the step at cursor c, and for int4 the
 // (s, z) / (s, min) pair of each lane's group.
 template <int WF, int T, bool SILU>
-__device__ __forceinline__ void issue_step(const GemvParams& p, StepCursor c, int ntl, int cpw, int tile0, int wave,
-                                           int NW, int c8, int r, u32x4 (&buf)[T], uint32_t (&sc)[T]) {
-    if (c.tl >= ntl) {
-        c.tl = ntl - 1;
-        c.jj = cpw - 1;
-    }
-    const int ch = wave + c.jj * NW;
+__device__ __forceinline__ void issue_step(const GemvParams& p, StepCursor c, int tile0, int c8, int r,
+                                           u32x4 (&buf)[T], uint32_t (&sc)[T]) {
+    const int ch = c.ch;
     const int colbase = (tile0 + c.tl) * 8;
     const uint8_t* base = p.w + (int64_t)colbase * p.row_bytes + ch * 128;  // uniform
     const int lr = min(r, p.n_out - 1 - colbase);                            // partial last tile
     const int lk = min(c8 * 16, (int)p.row_bytes - 16 - ch * 128);            // K tail
-    const uint32_t off = (uint32_t)(lr * (int)p.row_bytes + lk);
+    // 24-bit multiply (lr < 8, row_bytes < 2^24): a 64-bit mad here would
+    // read an unrelated register and force a wait on every load in flight
+    const uint32_t off = __umul24((uint32_t)lr, (uint32_t)p.row_bytes) + (uint32_t)lk;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         const uint8_t* bt = SILU && t ? base + (int64_t)p.n_out * p.row_bytes : base;
         buf[t] = ldg16(bt + off);
     }
-    if (is_int4(WF)) {
+    if (WF == WF_I4ZP) {
         const int g = ((ch * 128 + lk) * 2) >> p.glog2;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int row = colbase + lr + (SILU && t ? p.n_out : 0);
-            if (WF == WF_I4ZP) {
-                sc[t] = reinterpret_cast<const uint32_t*>(p.sc0)[(int64_t)g * p.N + row];
-            } else {
-                sc[t] = (uint32_t)reinterpret_cast<const uint16_t*>(p.sc0)[(int64_t)row * p.G + g] |
-                        ((uint32_t)reinterpret_cast<const uint16_t*>(p.sc1)[(int64_t)row * p.G + g] << 16);
-            }
+            sc[t] = reinterpret_cast<const uint32_t*>(p.sc0)[(int64_t)g * p.N + row];
+        }
+    } else if (WF == WF_I4MIN) {
+        const int g = ((ch * 128 + lk) * 2) >> p.glog2;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int row = colbase + lr + (SILU && t ? p.n_out : 0);
+            sc[t] = (uint32_t)reinterpret_cast<const uint16_t*>(p.sc0)[(int64_t)row * p.G + g] |
+                    ((uint32_t)reinterpret_cast<const uint16_t*>(p.sc1)[(int64_t)row * p.G + g] << 16);
         }
     }
 }
 
 template <int WF, int M, int T>
-__device__ __forceinline__ void consume_step(const GemvParams& p, StepCursor c, int tile0, int wave, int NW, int c8,
-                                             int r, int xe, const uint16_t* xs, const float* xsum,
-                                             const NibbleConsts& nc, const u32x4 (&buf)[T], const uint32_t (&scv)[T],
-                                             float (&acc)[T][M]) {
-    const int ch = wave + c.jj * NW;
+__device__ __forceinline__ void consume_step(const GemvParams& p, StepCursor c, int tile0, int c8, int r, int xe,
+                                             const uint16_t* xs, const float* xsum, const NibbleConsts& nc,
+                                             const u32x4 (&buf)[T], const uint32_t (&scv)[T], float (&acc)[T][M]) {
+    const int ch = c.ch;
     const int boff = ch * 128 + c8 * 16;
     if (!((tile0 + c.tl) * 8 + r < p.n_out && boff < p.row_bytes)) return;
     if (is_int4(WF)) {
@@ -406,8 +564,8 @@ __global__ void __launch_bounds__(kMaxThreads) gemv_persist(GemvParams p) {
     const int xe = x_row_elems(p.K, WF);
     const int tile0 = blockIdx.x * p.tpw;
     const int ntl = min(p.tpw, p.ntiles - tile0);
-    const int cpw = (p.nchunks - 1 - wave) / NW + 1;  // this wave's chunks per tile (host ensures NW <= nchunks)
-    const int S = ntl * cpw;                          // steps of this wave
+    const int nch = p.nchunks;
+    const int S = wave_steps(ntl, nch, NW, wave);  // this wave's steps (host ensures NW <= nchunks)
 
     const LdsLayout L = lds_layout(M, T, NW, p.K, WF, p.tpw);
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem + L.xs);
@@ -415,81 +573,51 @@ __global__ void __launch_bounds__(kMaxThreads) gemv_persist(GemvParams p) {
     float* red = reinterpret_cast<float*>(smem + L.red);
     float* nrm = reinterpret_cast<float*>(smem + L.nrm);
 
-    // 0. x (and gamma) loads first, then the first D steps of weights; the
-    //    scheduling barrier keeps every consumer of x below the weight loads.
-    u32x4 xr[kXB], gr[kXB];
-    issue_x<WF, M>(p, tid, nthr, xr, gr);
     u32x4 buf[D][T];
     uint32_t scb[D][T];
-    StepCursor ic{0, 0};
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-        issue_step<WF, T, SILU>(p, ic, ntl, cpw, tile0, wave, NW, c8, r, buf[d], scb[d]);
-        ic.advance(cpw);
-    }
+    auto issue = [&](int d, StepCursor c) { issue_step<WF, T, SILU>(p, c, tile0, c8, r, buf[d], scb[d]); };
+
+    // 0. x (and gamma) loads first, then the first D steps of weights.  The
+    //    first scheduling barrier keeps the x loads ahead of the weight loads
+    //    (vector loads retire in order, so x is then waited for without
+    //    waiting for the weights); the second keeps every consumer of x below
+    //    the weight loads.
+    u32x4 xr[kXB], gr[kXB];
+    issue_x<WF, M>(p, tid, nthr, xr, gr);
+    const EpiPrefetch<T> pre = epi_prefetch<WF, M, T, SILU, 8>(p, tile0, ntl, tid);
+    __builtin_amdgcn_sched_barrier(0);
+    StepCursor ic{0, wave};
+    pipeline_prime<D>(S, NW, nch, wave, ic, issue);
     __builtin_amdgcn_sched_barrier(0);
     // 1. x staging completes while the weights are in flight
     finish_x<WF, M>(p, xr, gr, xs, xsum, nrm, tid, nthr, wave, lane);
     __syncthreads();
 
-    // 2. rolling pipeline: consume a step, refill its slot D steps ahead
+    // 2. every step once; a wave's partial sums of a tile go to LDS after its
+    //    last step in that tile, reduced over the 8 lanes of each row
     const NibbleConsts nc;
     float acc[T][M];
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
         for (int m = 0; m < M; ++m) acc[t][m] = 0.0f;
-    StepCursor cc{0, 0};
-    for (int s0 = 0; s0 < S; s0 += D) {
+    pipeline_run<D>(S, NW, nch, wave, ic, issue, [&](int d, StepCursor c) {
+        consume_step<WF, M, T>(p, c, tile0, c8, r, xe, xs, xsum, nc, buf[d], scb[d], acc);
+        if (c.last_in_tile(NW, nch)) {
 #pragma unroll
-        for (int d = 0; d < D; ++d) {
-            if (s0 + d < S) {
-                consume_step<WF, M, T>(p, cc, tile0, wave, NW, c8, r, xe, xs, xsum, nc, buf[d], scb[d], acc);
-                if (cc.jj == cpw - 1) {
-                    // tile finished: reduce over the 8 lanes of each row, park in LDS
+            for (int t = 0; t < T; ++t)
 #pragma unroll
-                    for (int t = 0; t < T; ++t)
-#pragma unroll
-                        for (int m = 0; m < M; ++m) {
-                            const float v = sum8(acc[t][m]);
-                            if (c8 == 0) red[(((cc.tl * NW + wave) * T + t) * M + m) * 8 + r] = v;
-                            acc[t][m] = 0.0f;
-                        }
+                for (int m = 0; m < M; ++m) {
+                    const float v = sum8(acc[t][m]);
+                    if (c8 == 0) red[(((c.tl * NW + wave) * T + t) * M + m) * 8 + r] = v;
+                    acc[t][m] = 0.0f;
                 }
-                cc.advance(cpw);
-            }
-            issue_step<WF, T, SILU>(p, ic, ntl, cpw, tile0, wave, NW, c8, r, buf[d], scb[d]);
-            ic.advance(cpw);
         }
-    }
+    });
     __syncthreads();
 
-    // 3. epilogue: sum the waves' partials in a fixed order, apply 1/rms
-    for (int i = tid; i < ntl * M * 8; i += nthr) {
-        const int tl = i / (M * 8);
-        const int m = (i >> 3) % M, q = i & 7;
-        const int c = (tile0 + tl) * 8 + q;
-        if (c >= p.n_out) continue;
-        const float inv = row_inv_rms(p, nrm, NW, M, m);
-        float a[T];
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-            float v = 0.0f;
-            for (int w = 0; w < NW; ++w) v += red[(((tl * NW + w) * T + t) * M + m) * 8 + q];
-            v *= inv;
-            if (WF == WF_FP8) v *= reinterpret_cast<const float*>(p.sc0)[SILU ? c + t * p.n_out : c];
-            a[t] = v;
-        }
-        float o = SILU ? silu(a[0]) * a[T - 1] : a[0];
-        if (p.epi == BZ_EPI_RESIDUAL) {
-            o += p.res_f32 ? reinterpret_cast<const float*>(p.res)[m * p.ldr + c]
-                           : bf16_to_f32(reinterpret_cast<const uint16_t*>(p.res)[m * p.ldr + c]);
-        }
-        if (p.out_f32)
-            reinterpret_cast<float*>(p.out)[m * p.ldo + c] = o;
-        else
-            reinterpret_cast<uint16_t*>(p.out)[m * p.ldo + c] = f32_to_bf16(o);
-    }
+    // 3. epilogue
+    epilogue<WF, M, T, SILU, 8>(p, tile0, ntl, tid, nthr, NW, red, nrm, pre);
 }
 
 // ---------------------------------------------------------------------------

@@ -50,7 +50,7 @@ __host__ __device__ inline MfmaLds mfma_lds_layout(int M, int T, int NW, int K, 
     const int xe = mfma_x_row_elems(K, wf);
     MfmaLds L;
     L.xs = 0;
-    L.x128 = align16(M * xe * 2);
+    L.x128 = L.xs + align16(M * xe * 2);
     L.red = L.x128 + (i4 ? align16(M * (xe / 128) * 4) : 0);
     L.nrm = L.red + align16(tpw * NW * T * M * 16 * 4);
     L.total = L.nrm + align16(NW * M * 4);
@@ -104,37 +104,35 @@ __device__ __forceinline__ void finish_x_mfma(const GemvParams& p, const u32x4 (
     }
 }
 
-// Issue the T weight loads of the unit at cursor c (clamped past the end),
-// and for int4 the (s, z) / (s, min) pair of the unit's group for row j.
+// Issue the T weight loads of the unit at cursor c, and for int4 the (s, z) /
+// (s, min) pair of the unit's group for row j.
 template <int WF, int T, bool SILU>
-__device__ __forceinline__ void issue_unit(const GemvParams& p, StepCursor c, int ntl, int cpw, int tile0, int wave,
-                                           int NW, int j, int kb, u32x4 (&buf)[T], uint32_t (&sc)[T]) {
-    if (c.tl >= ntl) {
-        c.tl = ntl - 1;
-        c.jj = cpw - 1;
-    }
-    const int u = wave + c.jj * NW;
+__device__ __forceinline__ void issue_unit(const GemvParams& p, StepCursor c, int tile0, int j, int kb,
+                                           u32x4 (&buf)[T], uint32_t (&sc)[T]) {
+    const int u = c.ch;
     const int colbase = (tile0 + c.tl) * 16;
     const uint8_t* base = p.w + (int64_t)colbase * p.row_bytes + u * 64;  // uniform
     const int lr = min(j, p.n_out - 1 - colbase);                          // partial last tile
     const int lk = min(kb * 16, (int)p.row_bytes - 16 - u * 64);            // K tail (fp8 / bf16)
-    const uint32_t off = (uint32_t)(lr * (int)p.row_bytes + lk);
+    const uint32_t off = __umul24((uint32_t)lr, (uint32_t)p.row_bytes) + (uint32_t)lk;  // lr < 16
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         const uint8_t* bt = SILU && t ? base + (int64_t)p.n_out * p.row_bytes : base;
         buf[t] = ldg16(bt + off);
     }
-    if (is_int4(WF)) {
-        const int g = (u * 128) >> p.glog2;
+    const int g = (u * 128) >> p.glog2;  // one group per unit (group >= 128)
+    if (WF == WF_I4ZP) {
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int row = colbase + lr + (SILU && t ? p.n_out : 0);
-            if (WF == WF_I4ZP) {
-                sc[t] = reinterpret_cast<const uint32_t*>(p.sc0)[(int64_t)g * p.N + row];
-            } else {
-                sc[t] = (uint32_t)reinterpret_cast<const uint16_t*>(p.sc0)[(int64_t)row * p.G + g] |
-                        ((uint32_t)reinterpret_cast<const uint16_t*>(p.sc1)[(int64_t)row * p.G + g] << 16);
-            }
+            sc[t] = reinterpret_cast<const uint32_t*>(p.sc0)[(int64_t)g * p.N + row];
+        }
+    } else if (WF == WF_I4MIN) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int row = colbase + lr + (SILU && t ? p.n_out : 0);
+            sc[t] = (uint32_t)reinterpret_cast<const uint16_t*>(p.sc0)[(int64_t)row * p.G + g] |
+                    ((uint32_t)reinterpret_cast<const uint16_t*>(p.sc1)[(int64_t)row * p.G + g] << 16);
         }
     }
 }
@@ -143,10 +141,10 @@ template <int M>
 constexpr int kQM = M < 4 ? M : 4;  // x rows a lane's accumulator holds that can be < M
 
 template <int WF, int M, int T>
-__device__ __forceinline__ void consume_unit(const GemvParams& p, StepCursor c, int wave, int NW, int j, int kb,
-                                             int xe, const uint16_t* xs, const float* x128, const NibbleConsts& nc,
+__device__ __forceinline__ void consume_unit(const GemvParams& p, StepCursor c, int j, int kb, int xe,
+                                             const uint16_t* xs, const float* x128, const NibbleConsts& nc,
                                              const u32x4 (&buf)[T], const uint32_t (&scv)[T], f32x4_t (&acc)[T]) {
-    const int u = wave + c.jj * NW;
+    const int u = c.ch;
     const int am = min(j, M - 1);  // x row this lane supplies to the A operand
     if (is_int4(WF)) {
         u32x4 a[4];
@@ -208,8 +206,7 @@ __global__ void __launch_bounds__(kMaxThreads) gemv_mfma(GemvParams p) {
     const int nunits = (int)((p.row_bytes + 63) / 64);
     const int tile0 = blockIdx.x * p.tpw;
     const int ntl = min(p.tpw, p.ntiles - tile0);
-    const int cpw = (nunits - 1 - wave) / NW + 1;  // this wave's units per tile (host ensures NW <= nunits)
-    const int S = ntl * cpw;
+    const int S = wave_steps(ntl, nunits, NW, wave);  // host ensures NW <= nunits
 
     const MfmaLds L = mfma_lds_layout(M, T, NW, p.K, WF, p.tpw);
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem + L.xs);
@@ -217,79 +214,46 @@ __global__ void __launch_bounds__(kMaxThreads) gemv_mfma(GemvParams p) {
     float* red = reinterpret_cast<float*>(smem + L.red);
     float* nrm = reinterpret_cast<float*>(smem + L.nrm);
 
+    u32x4 buf[D][T];
+    uint32_t scb[D][T];
+    auto issue = [&](int d, StepCursor c) { issue_unit<WF, T, SILU>(p, c, tile0, j, kb, buf[d], scb[d]); };
+
     // 0. x and gamma first, then the first D units of weights (+ scales)
     u32x4 xr[kXB], gr[kXB];
     issue_x<WF, M>(p, tid, nthr, xr, gr);
-    u32x4 buf[D][T];
-    uint32_t scb[D][T];
-    StepCursor ic{0, 0};
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-        issue_unit<WF, T, SILU>(p, ic, ntl, cpw, tile0, wave, NW, j, kb, buf[d], scb[d]);
-        ic.advance(cpw);
-    }
+    const EpiPrefetch<T> pre = epi_prefetch<WF, M, T, SILU, 16>(p, tile0, ntl, tid);
+    __builtin_amdgcn_sched_barrier(0);
+    StepCursor ic{0, wave};
+    pipeline_prime<D>(S, NW, nunits, wave, ic, issue);
     __builtin_amdgcn_sched_barrier(0);
     // 1. staging completes while the weights are in flight
     finish_x_mfma<WF, M>(p, xr, gr, xs, x128, nrm, tid, nthr, wave, lane);
     __syncthreads();
 
-    // 2. rolling pipeline
+    // 2. every unit once; a wave's partial sums of a tile go to LDS after its
+    //    last unit in that tile
     const NibbleConsts nc;
     f32x4_t acc[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    StepCursor cc{0, 0};
-    for (int s0 = 0; s0 < S; s0 += D) {
+    pipeline_run<D>(S, NW, nunits, wave, ic, issue, [&](int d, StepCursor c) {
+        consume_unit<WF, M, T>(p, c, j, kb, xe, xs, x128, nc, buf[d], scb[d], acc);
+        if (c.last_in_tile(NW, nunits)) {
 #pragma unroll
-        for (int d = 0; d < D; ++d) {
-            if (s0 + d < S) {
-                consume_unit<WF, M, T>(p, cc, wave, NW, j, kb, xe, xs, x128, nc, buf[d], scb[d], acc);
-                if (cc.jj == cpw - 1) {
-                    // tile finished: park this wave's partial sums in LDS
+            for (int t = 0; t < T; ++t) {
 #pragma unroll
-                    for (int t = 0; t < T; ++t) {
-#pragma unroll
-                        for (int q = 0; q < kQM<M>; ++q) {
-                            const int m = 4 * kb + q;
-                            if (m < M) red[(((cc.tl * NW + wave) * T + t) * M + m) * 16 + j] = acc[t][q];
-                        }
-                        acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-                    }
+                for (int q = 0; q < kQM<M>; ++q) {
+                    const int m = 4 * kb + q;
+                    if (m < M) red[(((c.tl * NW + wave) * T + t) * M + m) * 16 + j] = acc[t][q];
                 }
-                cc.advance(cpw);
+                acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
             }
-            issue_unit<WF, T, SILU>(p, ic, ntl, cpw, tile0, wave, NW, j, kb, buf[d], scb[d]);
-            ic.advance(cpw);
         }
-    }
+    });
     __syncthreads();
 
-    // 3. epilogue: sum the waves' partials in a fixed order, apply 1/rms
-    for (int i = tid; i < ntl * M * 16; i += nthr) {
-        const int tl = i / (M * 16);
-        const int m = (i >> 4) % M, q = i & 15;
-        const int c = (tile0 + tl) * 16 + q;
-        if (c >= p.n_out) continue;
-        const float inv = row_inv_rms(p, nrm, NW, M, m);
-        float a[T];
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-            float v = 0.0f;
-            for (int w = 0; w < NW; ++w) v += red[(((tl * NW + w) * T + t) * M + m) * 16 + q];
-            v *= inv;
-            if (WF == WF_FP8) v *= reinterpret_cast<const float*>(p.sc0)[SILU ? c + t * p.n_out : c];
-            a[t] = v;
-        }
-        float o = SILU ? silu(a[0]) * a[T - 1] : a[0];
-        if (p.epi == BZ_EPI_RESIDUAL) {
-            o += p.res_f32 ? reinterpret_cast<const float*>(p.res)[m * p.ldr + c]
-                           : bf16_to_f32(reinterpret_cast<const uint16_t*>(p.res)[m * p.ldr + c]);
-        }
-        if (p.out_f32)
-            reinterpret_cast<float*>(p.out)[m * p.ldo + c] = o;
-        else
-            reinterpret_cast<uint16_t*>(p.out)[m * p.ldo + c] = f32_to_bf16(o);
-    }
+    // 3. epilogue
+    epilogue<WF, M, T, SILU, 16>(p, tile0, ntl, tid, nthr, NW, red, nrm, pre);
 }
 
 template <int WF, int M, int T, int D, bool SILU>
