@@ -1,11 +1,20 @@
 // Host dispatcher of the streaming decode GEMV (C ABI entry bz_gemv).  The
-// kernels are in bz_gemv_kernel.h (dot2 path) and bz_gemv_mfma.h
-// (matrix-core path); their instances live in bz_gemv_{,mfma_}<fmt>.hip.
-#include "bz_gemv_mfma.h"
+// kernels are in bz_gemv_kernel.h (dot2 path), bz_gemv_mfma.h (bf16
+// matrix-core path) and bz_gemv_i8.h (int8 matrix-core path for int4
+// weights); their instances live in bz_gemv_{,mfma_,i8_}<fmt>.hip.
+#include "bz_gemv_i8.h"
 
 namespace bz {
 
-static int launch_wf(int wf, bool mfma, const GemvParams& p, const Launch& l, hipStream_t st) {
+enum { PATH_DOT2 = 1, PATH_MFMA = 2, PATH_I8 = 3 };
+
+static int launch_wf(int wf, int path, const GemvParams& p, const Launch& l, hipStream_t st) {
+    if (path == PATH_I8) {
+        if (wf == WF_I4ZP) return launch_i8_i4zp(p, l, st);
+        if (wf == WF_I4MIN) return launch_i8_i4min(p, l, st);
+        return BZ_ERR_INVALID_ARG;
+    }
+    const bool mfma = path == PATH_MFMA;
     switch (wf) {
         case WF_I4ZP: return mfma ? launch_mfma_i4zp(p, l, st) : launch_i4zp(p, l, st);
         case WF_I4MIN: return mfma ? launch_mfma_i4min(p, l, st) : launch_i4min(p, l, st);
@@ -80,14 +89,22 @@ extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
 
     const bool silu = epi == BZ_EPI_SILU_GATE;
     const int T = silu ? 2 : 1;
-    // Path: the matrix-core kernel unless the int4 group is smaller than one
-    // 64-byte unit (128 k), which only the dot2 kernel can scale.
+    // Paths: the matrix-core kernels need 64-byte units that hold one int4
+    // group (group >= 128); the int8 one also whole units (K % 128 == 0).
     const bool mfma_ok = !i4 || d->group >= 128;
-    if (d->cfg_path < 0 || d->cfg_path > 2) return BZ_ERR_INVALID_ARG;
-    if (d->cfg_path == 2 && !mfma_ok) return BZ_ERR_UNSUPPORTED;
-    // Automatic choice: dot2 for a single row (its VALU work is smallest),
-    // the matrix cores once several rows share each unpacked weight.
-    const bool mfma = d->cfg_path == 0 ? (mfma_ok && M > 1) : d->cfg_path == 2;
+    const bool i8_ok = i4 && d->group >= 128 && K % 128 == 0;
+    if (d->cfg_path < 0 || d->cfg_path > 3) return BZ_ERR_INVALID_ARG;
+    if ((d->cfg_path == 2 && !mfma_ok) || (d->cfg_path == 3 && !i8_ok)) return BZ_ERR_UNSUPPORTED;
+    // Automatic choice (measured on MI355X, M = 1..16): the int8 matrix-core
+    // path for several rows over short rows (K <= 4096: every workgroup
+    // stages all of x, 2 bytes per element, which long rows make costly);
+    // the dot2 kernel for a single-row SiLU-gate pair; the bf16 matrix-core
+    // path otherwise.
+    const int path = d->cfg_path                          ? d->cfg_path
+                     : (i8_ok && M > 1 && K <= 4096)      ? PATH_I8
+                     : (mfma_ok && !(silu && M == 1))     ? PATH_MFMA
+                                                           : PATH_DOT2;
+    const bool mfma = path != PATH_DOT2;
     const int cols_per_tile = mfma ? 16 : 8;
     const int unit_bytes = mfma ? 64 : 128;
     const int nunits = (int)((row_bytes + unit_bytes - 1) / unit_bytes);
@@ -97,18 +114,23 @@ extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
     l.nw = d->cfg_waves ? d->cfg_waves : (nunits > kMaxWaves ? kMaxWaves : nunits);
     if (l.nw < 1 || l.nw > kMaxWaves) return BZ_ERR_INVALID_ARG;
     if (l.nw > nunits) l.nw = nunits;  // every wave owns at least one unit of each tile
-    int tpw = d->cfg_tiles ? d->cfg_tiles : (ntiles + kTargetWorkgroups - 1) / kTargetWorkgroups;
-    if (tpw < 1) return BZ_ERR_INVALID_ARG;
-    if (tpw > ntiles) tpw = ntiles;
-    l.grid = (unsigned)((ntiles + tpw - 1) / tpw);
+    // Workgroups: one per cfg_tiles tiles, or ceil(ntiles / 256) tiles each
+    // (about one workgroup per CU); each takes a balanced share of the tiles
+    // (tpw = the largest share).
+    if (d->cfg_tiles < 0) return BZ_ERR_INVALID_ARG;
+    const int want = d->cfg_tiles ? d->cfg_tiles : (ntiles + kTargetWorkgroups - 1) / kTargetWorkgroups;
+    const int grid = (ntiles + want - 1) / want;
+    const int tpw = (ntiles + grid - 1) / grid;
+    l.grid = (unsigned)grid;
     if (d->cfg_depth && ((d->cfg_depth != 2 && d->cfg_depth != 4 && d->cfg_depth != 8 && d->cfg_depth != 16) ||
-                         d->cfg_depth * T > kMaxLoadsInFlight))
+                         d->cfg_depth * T > kMaxLoadsInFlight || (path == PATH_I8 && d->cfg_depth > 8)))
         return BZ_ERR_INVALID_ARG;
     // (argument validation ends here: the rest may query the device)
-    // Measured on MI355X: 8 waves x 2 steps in flight per wave stream the
-    // decode shapes best (deeper per-wave pipelines only lengthen the queue
-    // the x loads wait in); bf16 rows, with fewer k per byte, prefer 4 steps.
-    l.depth = d->cfg_depth ? d->cfg_depth : (wf == BZ_W_BF16 && T == 1 ? 4 : 2);
+    // Measured on MI355X: 8 waves with 2 steps in flight per wave for a
+    // SiLU-gate pair (each step loads two tiles) and 4 for single tiles on
+    // the matrix-core paths; deeper pipelines only lengthen the queue the x
+    // loads wait in.
+    l.depth = d->cfg_depth ? d->cfg_depth : (T == 1 && (path != PATH_DOT2 || wf == BZ_W_BF16) ? 4 : 2);
     const int lds_lim = device_lds_limit();
     const int nchunks = (int)((row_bytes + 127) / 128);
 
@@ -136,16 +158,22 @@ extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
     p.norm = d->gamma != nullptr;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const size_t osz = p.out_f32 ? 4 : 2, rsz = p.res_f32 ? 4 : 2;
-    for (int m0 = 0; m0 < M; m0 += kMaxRowsPerLaunch) {
-        l.M = (M - m0) < kMaxRowsPerLaunch ? (M - m0) : kMaxRowsPerLaunch;
-        const int lds = mfma ? mfma_lds_layout(l.M, T, l.nw, K, wf, tpw).total
-                             : lds_layout(l.M, T, l.nw, K, wf, tpw).total;
+    // rows per launch: 4 on the bf16 paths; up to the 16 rows of the MFMA A
+    // operand on the int8 path, as many as its LDS (2 bytes of x per
+    // element) allows
+    const int rows = path == PATH_I8 ? i8_max_rows(K, lds_lim, T, l.nw, tpw) : kMaxRowsPerLaunch;
+    if (rows < 1) return BZ_ERR_UNSUPPORTED;
+    for (int m0 = 0; m0 < M; m0 += rows) {
+        l.M = (M - m0) < rows ? (M - m0) : rows;
+        const int lds = path == PATH_I8 ? i8_lds_layout(l.M, T, l.nw, K, tpw).total
+                        : mfma          ? mfma_lds_layout(l.M, T, l.nw, K, wf, tpw).total
+                                        : lds_layout(l.M, T, l.nw, K, wf, tpw).total;
         if (lds > lds_lim) return BZ_ERR_UNSUPPORTED;
         l.lds = (size_t)lds;
         p.x = static_cast<const uint16_t*>(d->x) + (int64_t)m0 * d->ldx;
         p.out = static_cast<uint8_t*>(d->out) + (int64_t)m0 * d->ldo * osz;
         p.res = d->residual ? static_cast<const uint8_t*>(d->residual) + (int64_t)m0 * d->ldr * rsz : nullptr;
-        const int rc = launch_wf(wf, mfma, p, l, st);
+        const int rc = launch_wf(wf, path, p, l, st);
         if (rc != BZ_OK) return rc;
     }
     return BZ_OK;

@@ -77,7 +77,7 @@ struct GemvParams {
     int64_t ldo;
     float eps;
     int N, K, G, glog2, n_out, nchunks;
-    int ntiles, tpw;  // tiles of 8 (dot2) or 16 (MFMA) output columns, tiles per workgroup
+    int ntiles, tpw;  // tiles of 8 (dot2) or 16 (MFMA) output columns; most tiles a workgroup owns
     int epi, out_f32, res_f32, norm;
 };
 
@@ -384,15 +384,26 @@ __device__ __forceinline__ StepCursor step_cursor(int s, int NW, int nch, int wa
 // unconditionally, which keeps the compiler's vector-memory wait counts
 // exact (each consume waits only for its own slot); the tail issues behind a
 // wave-uniform branch.
-template <int D, typename IssueFn>
+// Slots [B, E) of the prime (the kernels issue all D before staging x:
+// issuing one step first and the rest after staging measured slower).
+template <int B, int E, typename IssueFn>
 __device__ __forceinline__ void pipeline_prime(int S, int NW, int nch, int wave, StepCursor& ic, IssueFn issue) {
     const StepCursor last = step_cursor(S - 1, NW, nch, wave);
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
+    for (int d = B; d < E; ++d) {
         issue(d, d < S ? ic : last);
         ic.advance(NW, nch);
     }
 }
+
+// This workgroup's tiles: a balanced share (counts differ by at most one).
+struct TileRange {
+    int tile0, ntl;
+    __device__ __forceinline__ TileRange(int ntiles) {
+        tile0 = (int)(((int64_t)blockIdx.x * ntiles) / gridDim.x);
+        ntl = (int)(((int64_t)(blockIdx.x + 1) * ntiles) / gridDim.x) - tile0;
+    }
+};
 
 template <int D, typename IssueFn, typename ConsumeFn>
 __device__ __forceinline__ void pipeline_run(int S, int NW, int nch, int wave, StepCursor ic, IssueFn issue,
@@ -562,8 +573,8 @@ __global__ void __launch_bounds__(kMaxThreads) gemv_persist(GemvParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c8 = lane & 7, r = lane >> 3;
     const int xe = x_row_elems(p.K, WF);
-    const int tile0 = blockIdx.x * p.tpw;
-    const int ntl = min(p.tpw, p.ntiles - tile0);
+    const TileRange tr(p.ntiles);
+    const int tile0 = tr.tile0, ntl = tr.ntl;
     const int nch = p.nchunks;
     const int S = wave_steps(ntl, nch, NW, wave);  // this wave's steps (host ensures NW <= nchunks)
 
@@ -587,7 +598,7 @@ __global__ void __launch_bounds__(kMaxThreads) gemv_persist(GemvParams p) {
     const EpiPrefetch<T> pre = epi_prefetch<WF, M, T, SILU, 8>(p, tile0, ntl, tid);
     __builtin_amdgcn_sched_barrier(0);
     StepCursor ic{0, wave};
-    pipeline_prime<D>(S, NW, nch, wave, ic, issue);
+    pipeline_prime<0, D>(S, NW, nch, wave, ic, issue);
     __builtin_amdgcn_sched_barrier(0);
     // 1. x staging completes while the weights are in flight
     finish_x<WF, M>(p, xr, gr, xs, xsum, nrm, tid, nthr, wave, lane);

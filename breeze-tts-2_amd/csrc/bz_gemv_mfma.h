@@ -204,8 +204,8 @@ __global__ void __launch_bounds__(kMaxThreads) gemv_mfma(GemvParams p) {
     const int j = lane & 15, kb = lane >> 4;
     const int xe = mfma_x_row_elems(p.K, WF);
     const int nunits = (int)((p.row_bytes + 63) / 64);
-    const int tile0 = blockIdx.x * p.tpw;
-    const int ntl = min(p.tpw, p.ntiles - tile0);
+    const TileRange tr(p.ntiles);
+    const int tile0 = tr.tile0, ntl = tr.ntl;
     const int S = wave_steps(ntl, nunits, NW, wave);  // host ensures NW <= nunits
 
     const MfmaLds L = mfma_lds_layout(M, T, NW, p.K, WF, p.tpw);
@@ -224,7 +224,7 @@ __global__ void __launch_bounds__(kMaxThreads) gemv_mfma(GemvParams p) {
     const EpiPrefetch<T> pre = epi_prefetch<WF, M, T, SILU, 16>(p, tile0, ntl, tid);
     __builtin_amdgcn_sched_barrier(0);
     StepCursor ic{0, wave};
-    pipeline_prime<D>(S, NW, nunits, wave, ic, issue);
+    pipeline_prime<0, D>(S, NW, nunits, wave, ic, issue);
     __builtin_amdgcn_sched_barrier(0);
     // 1. staging completes while the weights are in flight
     finish_x_mfma<WF, M>(p, xr, gr, xs, x128, nrm, tid, nthr, wave, lane);

@@ -87,8 +87,11 @@ typedef enum bz_dtype {
  * per-shape rule; otherwise they force the streaming kernel's pipeline depth
  * (2, 4, 8 or 16 steps of weight loads in flight per wave; at most 8 for
  * SiLU-gate), waves per workgroup (1..8), output tiles per workgroup (>= 1)
- * and arithmetic path (1 = v_dot2 kernel, 8-column tiles; 2 = MFMA kernel,
- * 16-column tiles, needs an int4 group >= 128).  Used by tuning sweeps.
+ * and arithmetic path (1 = v_dot2 kernel, 8-column tiles; 2 = bf16 MFMA
+ * kernel, 16-column tiles, needs an int4 group >= 128; 3 = int8 MFMA kernel
+ * for int4 weights, group >= 128 and K % 128 == 0, x held as two int8
+ * planes per row (about 16 significant bits), up to 16 rows per launch).
+ * Used by tuning sweeps.
  */
 typedef struct bz_gemv_desc {
     int32_t abi_version;      /* must be BZ_ABI_VERSION */

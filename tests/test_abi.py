@@ -123,7 +123,11 @@ def _desc(L, **kw):
         ({"x": (1 << 20) + 2}, "ERR_ALIGNMENT"),
         ({"w": (1 << 20) + 8}, "ERR_ALIGNMENT"),
         ({"ldx": 260}, "ERR_ALIGNMENT"),                       # rows not 16-byte aligned
-        ({"cfg_path": 3}, "ERR_INVALID_ARG"),
+        ({"cfg_path": 4}, "ERR_INVALID_ARG"),
+        ({"cfg_path": 3, "wfmt": 2}, "ERR_UNSUPPORTED"),               # int8 path is int4-only
+        ({"cfg_path": 3, "group": 64}, "ERR_UNSUPPORTED"),             # and needs group >= 128
+        ({"cfg_path": 3, "cfg_depth": 16}, "ERR_INVALID_ARG"),         # int8 path: depth <= 8
+        ({"cfg_tiles": -1}, "ERR_INVALID_ARG"),
         ({"cfg_depth": 3}, "ERR_INVALID_ARG"),
         ({"cfg_depth": 16, "epilogue": 1}, "ERR_INVALID_ARG"),  # 2 x 16 loads in flight
         ({"cfg_waves": 9}, "ERR_INVALID_ARG"),
