@@ -89,6 +89,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-step", action="store_true", help="skip the 26-layer decode step detail")
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-config GEMV table (C1-C4)")
     ap.add_argument("--profile-gateup", action="store_true",
                     help="only launch the gate|up GEMV (eagerly) and a 256 MiB copy, for counter runs")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -243,7 +244,10 @@ def main() -> int:
 
     # ---- full synthetic decode step (26 int4 layers + bf16 head), M = 1
     if not args.no_step:
-        detail["decode_step"] = decode_step(torch, G, dev, log)
+        detail["decode_step"] = decode_step(torch, G, dev, log, 1)
+        detail["decode_step_m2"] = decode_step(torch, G, dev, log, 2)
+    if not args.no_configs:
+        detail["configs"] = config_table(torch, G, dev, log)
 
     # ---- CPU baseline: same MLP step on the host cores (bounded sample)
     cpu = None
@@ -329,12 +333,77 @@ def pmc_summary(fetch_dir: str, write_dir: str) -> int:
     return 0
 
 
-def decode_step(torch, G, dev, log) -> dict:
+# (name, weight format, N, K, epilogue, RMSNorm prologue, M values): the
+# GEMV shapes of the benchmark configurations C1-C4
+CONFIG_SHAPES = [
+    ("C1 rms->int4 K2048 N2048", "int4", 2048, 2048, 0, True, (1, 2)),
+    ("C2 rms->int4 gate|up K2560 N2x10240 silu", "int4", 20480, 2560, 1, True, (1, 2)),
+    ("C2 int4 down K10240 N2560", "int4", 2560, 10240, 0, False, (1, 2)),
+    ("C3 rms->fp8 qkv K2560 N4096", "fp8", 4096, 2560, 0, True, (1, 2)),
+    ("C3 fp8 o_proj K4096 N2560", "fp8", 2560, 4096, 0, False, (1, 2)),
+    ("C3 rms->fp8 gate|up K2560 N2x10240 silu", "fp8", 20480, 2560, 1, True, (1, 2)),
+    ("C3 fp8 down K10240 N2560", "fp8", 2560, 10240, 0, False, (1, 2)),
+    ("C4 int4 K2560 N20480", "int4", 20480, 2560, 0, False, (4, 8, 16, 32)),
+    ("C4 int4 K10240 N2560", "int4", 2560, 10240, 0, False, (4, 8, 16, 32)),
+    ("C4 fp8 K2560 N20480", "fp8", 20480, 2560, 0, False, (4, 8, 16, 32)),
+    ("C4 fp8 K10240 N2560", "fp8", 2560, 10240, 0, False, (4, 8, 16, 32)),
+]
+
+
+def config_table(torch, G, dev, log) -> list:
+    """Each GEMV of C1-C4 (synthetic weights N(0, 0.02), int4 symmetric g128
+    or fp8 e4m3 per-row, bf16 x N(0, 1)), timed as HIP-graph replays over
+    weight copies rotating through >= 1 GiB: µs per call, algorithmic GB/s
+    and the fraction of the 8 TB/s bytes-moved roofline."""
+    from breeze_amd.fused.kernels import graph_time_us
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    rows = []
+    for name, fmt, N, K, epi, norm, Ms in CONFIG_SHAPES:
+        w = torch.randn(N, K, device=dev, generator=gen) * 0.02
+        if fmt == "int4":
+            p, sz, _ = G.quantize_int4_device(w, GROUP, True, G.W_INT4_ZP)
+            base = (p, sz)
+            wfmt, bits = G.W_INT4_ZP, 4
+        else:
+            c, sc = G.quantize_fp8_device(w, 1e-12)
+            base = (c.view(torch.uint8), sc)
+            wfmt, bits = G.W_FP8, 8
+        del w
+        wbytes = sum(t.numel() * t.element_size() for t in base)
+        ncopy = max(2, -(-(1 << 30) // wbytes))
+        copies = [tuple(t.clone() for t in base) for _ in range(ncopy)]
+        gamma = (1 + 0.1 * torch.randn(K, device=dev, generator=gen)).to(torch.bfloat16) if norm else None
+        n_out = N // 2 if epi == 1 else N
+        for M in Ms:
+            x = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
+            out = torch.empty(M, n_out, device=dev, dtype=torch.bfloat16)
+            st = {"i": 0}
+
+            def call():
+                c = copies[st["i"] % ncopy]
+                st["i"] += 1
+                G.gemv(x, c[0], wfmt, N, sc0=c[1], group=GROUP, gamma=gamma, eps=EPS, epilogue=epi, out=out)
+
+            us = graph_time_us(call, iters=2 * ncopy)
+            nbytes = algo_bytes(bits, N, K, M, norm, epi)
+            roof = nbytes / HBM_PEAK_GBPS / 1e3
+            rows.append({"config": name, "M": M, "us": round(us, 2), "gbps": round(nbytes / us / 1e3, 1),
+                         "roofline_us": round(roof, 2), "frac": round(roof / us, 3)})
+            log(f"{name:42s} M={M:2d}: {us:7.2f} us  {nbytes / us / 1e3:6.0f} GB/s  "
+                f"({roof / us * 100:4.1f}% of roofline)")
+        del copies
+        torch.cuda.empty_cache()
+    return rows
+
+
+def decode_step(torch, G, dev, log, M: int = 1) -> dict:
     """26 decoder layers (hidden 2560, 16x256 q heads, 4 KV heads, MLP 10240)
     of int4 group-128 weights: RMSNorm->QKV, attention replaced by a copy of
     [M, 4096], o_proj + residual, RMSNorm->gate|up SiLU-gate, down + residual;
     then a final RMSNorm -> bf16 head K2560 N8192.  One HIP graph per step."""
-    H, QKV, ATT, MLP, LAYERS, VOCAB, M = 2560, 6144, 4096, 10240, 26, 8192, 1
+    H, QKV, ATT, MLP, LAYERS, VOCAB = 2560, 6144, 4096, 10240, 26, 8192
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
 
@@ -394,7 +463,7 @@ def decode_step(torch, G, dev, log) -> dict:
     torch.cuda.synchronize()
     us = s_ev.elapsed_time(e_ev) * 1e3 / reps
     roof = nbytes / HBM_PEAK_GBPS / 1e3
-    log(f"decode step (26 layers + head, M=1): {us:.1f} us, roofline {roof:.1f} us ({us / roof:.2f}x)")
+    log(f"decode step (26 layers + head, M={M}): {us:.1f} us, roofline {roof:.1f} us ({us / roof:.2f}x)")
     del g, layers, head
     torch.cuda.empty_cache()
     return {"us": round(us, 2), "algorithmic_bytes": nbytes, "roofline_us": round(roof, 2),
