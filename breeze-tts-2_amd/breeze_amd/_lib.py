@@ -1,4 +1,5 @@
-"""ctypes binding of libbzgemv.so (the C ABI declared in include/bz_gemv.h).
+"""ctypes binding of libbzgemv.so (the C ABI declared in include/bz_gemv.h and
+include/bz_attn.h).
 
 torch is imported before the library is opened: both link the HIP runtime by
 its SONAME (libamdhip64.so.7), so the library binds to the runtime torch has
@@ -23,6 +24,7 @@ ERR_INVALID_ARG, ERR_SHAPE, ERR_ALIGNMENT, ERR_UNSUPPORTED, ERR_LAUNCH, ERR_ABI 
 W_INT4_ZP, W_INT4_MIN, W_FP8, W_BF16 = 0, 1, 2, 3
 EPI_NONE, EPI_SILU_GATE, EPI_RESIDUAL = 0, 1, 2
 DT_BF16, DT_F32 = 0, 1
+MASK_BOOL = 2  # include/bz_attn.h
 
 EXPORTS = (
     "bz_abi_version",
@@ -34,6 +36,10 @@ EXPORTS = (
     "bz_quantize_int4",
     "bz_quantize_fp8",
     "bz_dequant",
+    "bz_qkv_rope_cache",
+    "bz_attn_decode",
+    "bz_attn_workspace",
+    "bz_attn_default_split",
 )
 
 
@@ -97,6 +103,16 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.bz_quantize_fp8.argtypes = [vp, i32, i32, i32, f32, vp, vp, vp]
     lib.bz_dequant.restype = ctypes.c_int
     lib.bz_dequant.argtypes = [i32, vp, vp, vp, i32, i32, i32, vp, vp]
+    lib.bz_qkv_rope_cache.restype = ctypes.c_int
+    lib.bz_qkv_rope_cache.argtypes = [vp, i64, i32, i32, i32, i32, vp, vp, f32, vp, vp, i32, i64, vp, vp, vp, vp,
+                                      i32, i32, vp, vp]
+    lib.bz_attn_decode.restype = ctypes.c_int
+    lib.bz_attn_decode.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, i32, i64, vp, f32, i32, vp, vp, i64,
+                                   vp]
+    lib.bz_attn_workspace.restype = ctypes.c_size_t
+    lib.bz_attn_workspace.argtypes = [i32, i32, i32, i32]
+    lib.bz_attn_default_split.restype = ctypes.c_int32
+    lib.bz_attn_default_split.argtypes = [i32]
 
 
 def lib() -> ctypes.CDLL:

@@ -34,6 +34,7 @@ from ..gemv import (
     quantize_fp8_device,
     quantize_int4_device,
 )
+from ..attention import attention_step
 from ..gemv import rmsnorm as _rmsnorm
 from ..gemv import silu_mul as _silu_mul
 
@@ -45,6 +46,7 @@ __all__ = [
     "pack_int4",
     "pack_fp8",
     "rms_gemv",
+    "attention_step",
     "rmsnorm",
     "silu_mul",
     "graph_time_us",

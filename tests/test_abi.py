@@ -1,5 +1,5 @@
 """The C ABI of libbzgemv.so without a GPU: the library loads, exports every
-function include/bz_gemv.h declares, the ctypes descriptor matches the C
+function include/bz_gemv.h and include/bz_attn.h declare, the ctypes descriptor matches the C
 struct byte for byte, and argument validation answers with the documented
 status codes before anything touches a device."""
 
@@ -15,6 +15,7 @@ import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "bz_gemv.h"
+HEADERS = (HEADER, ROOT / "include" / "bz_attn.h")
 
 
 @pytest.fixture(scope="module")
@@ -29,9 +30,11 @@ def L():
 
 
 def declared_functions() -> list[str]:
-    text = HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(bz_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(bz_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_declares_the_binding_exports(L):
@@ -161,6 +164,79 @@ def test_aux_validation(L):
     assert lib.bz_dequant(0, f, f, None, 8, 200, 128, f, None) == L.ERR_SHAPE
     assert lib.bz_dequant(0, f + 4, f, None, 8, 256, 128, f, None) == L.ERR_ALIGNMENT
     assert lib.bz_dequant(9, f, f, None, 8, 256, 128, f, None) == L.ERR_INVALID_ARG
+
+
+def _rope_args(L, **kw):
+    f = 1 << 20
+    a = dict(qkv=f, ld_qkv=24 * 64, B=1, HQ=16, HKV=4, D=64, qn=f, kn=f, eps=1e-6, cos=f, sin=f, cs_dtype=L.DT_BF16,
+             ld_cs=64, pos=f, q_out=f, kc=f, vc=f, S=32, cache_dtype=L.DT_BF16, seq_len=None, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize(
+    "kw,status",
+    [
+        ({"qkv": None}, "ERR_INVALID_ARG"),
+        ({"pos": None}, "ERR_INVALID_ARG"),
+        ({"kn": None}, "ERR_INVALID_ARG"),        # q and k norm weights come together
+        ({"HKV": 0}, "ERR_INVALID_ARG"),
+        ({"cs_dtype": 2}, "ERR_INVALID_ARG"),
+        ({"cache_dtype": 2}, "ERR_INVALID_ARG"),
+        ({"D": 63}, "ERR_SHAPE"),
+        ({"D": 2048, "ld_qkv": 24 * 2048}, "ERR_SHAPE"),
+        ({"ld_qkv": 24 * 64 - 1}, "ERR_SHAPE"),
+        ({"ld_cs": -1}, "ERR_SHAPE"),
+    ],
+)
+def test_rope_cache_validation(L, kw, status):
+    assert L.lib().bz_qkv_rope_cache(*_rope_args(L, **kw)) == getattr(L, status)
+
+
+def _attn_args(L, **kw):
+    f = 1 << 20
+    a = dict(q=f, kc=f, vc=f, cache_dtype=L.DT_BF16, B=2, HQ=16, HKV=4, D=256, S=512, mask=f, mask_dtype=L.DT_BF16,
+             ld_mask=512, pos=f, scale=0.0625, split=4, part=f, out=f, ld_out=4096, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize(
+    "kw,status",
+    [
+        ({"q": None}, "ERR_INVALID_ARG"),
+        ({"mask": None}, "ERR_INVALID_ARG"),
+        ({"HQ": 15}, "ERR_INVALID_ARG"),                 # HQ % HKV
+        ({"cache_dtype": 3}, "ERR_INVALID_ARG"),
+        ({"mask_dtype": 3}, "ERR_INVALID_ARG"),
+        ({"ld_mask": -1}, "ERR_SHAPE"),
+        ({"split": 0}, "ERR_INVALID_ARG"),
+        ({"split": 65}, "ERR_INVALID_ARG"),
+        ({"part": None}, "ERR_INVALID_ARG"),             # split > 1 needs the workspace
+        ({"ld_mask": 100}, "ERR_SHAPE"),
+        ({"ld_out": 4095}, "ERR_SHAPE"),
+        ({"D": 96, "ld_out": 16 * 96}, "ERR_UNSUPPORTED"),
+        ({"HQ": 32, "HKV": 1, "ld_out": 32 * 256}, "ERR_UNSUPPORTED"),   # G > 16
+        ({"D": 512, "HKV": 2, "ld_out": 16 * 512}, "ERR_UNSUPPORTED"),   # G > 4 at D = 512
+        ({"q": (1 << 20) + 4}, "ERR_ALIGNMENT"),
+        ({"kc": (1 << 20) + 8}, "ERR_ALIGNMENT"),
+    ],
+)
+def test_attn_validation(L, kw, status):
+    assert L.lib().bz_attn_decode(*_attn_args(L, **kw)) == getattr(L, status)
+
+
+def test_attn_header_constants(L):
+    text = HEADERS[1].read_text()
+    assert int(re.search(r"#define\s+BZ_MASK_BOOL\s+(\d+)", text).group(1)) == L.MASK_BOOL
+    assert int(re.search(r"#define\s+BZ_ATTN_MAX_SPLIT\s+(\d+)", text).group(1)) == 64
+
+
+def test_attn_workspace_and_split(L):
+    lib = L.lib()
+    assert lib.bz_attn_workspace(2, 16, 256, 1) == 0
+    assert lib.bz_attn_workspace(2, 16, 256, 8) == 2 * 16 * 8 * 258 * 4
+    assert [lib.bz_attn_default_split(s) for s in (1, 128, 129, 1024, 2048, 8192)] == [1, 1, 2, 8, 16, 32]
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
