@@ -246,6 +246,7 @@ def main() -> int:
     if not args.no_step:
         detail["decode_step"] = decode_step(torch, G, dev, log, 1)
         detail["decode_step_m2"] = decode_step(torch, G, dev, log, 2)
+        detail["decode_step_attn"] = decode_step(torch, G, dev, log, 2, attn_pos=1023, cache_len=1024)
     if not args.no_configs:
         detail["configs"] = config_table(torch, G, dev, log)
 
@@ -398,12 +399,18 @@ def config_table(torch, G, dev, log) -> list:
     return rows
 
 
-def decode_step(torch, G, dev, log, M: int = 1) -> dict:
+def decode_step(torch, G, dev, log, M: int = 1, attn_pos: int | None = None, cache_len: int = 1024) -> dict:
     """26 decoder layers (hidden 2560, 16x256 q heads, 4 KV heads, MLP 10240)
     of int4 group-128 weights: RMSNorm->QKV, attention replaced by a copy of
     [M, 4096], o_proj + residual, RMSNorm->gate|up SiLU-gate, down + residual;
-    then a final RMSNorm -> bf16 head K2560 N8192.  One HIP graph per step."""
+    then a final RMSNorm -> bf16 head K2560 N8192.  One HIP graph per step.
+
+    With ``attn_pos`` the copy is replaced by the real decode attention step
+    (q/k RMSNorm + RoPE + cache write, attention over cache positions
+    [0, attn_pos] of a bf16 cache of ``cache_len`` positions per layer); its
+    algorithmic bytes (keys and values read once) join the roofline."""
     H, QKV, ATT, MLP, LAYERS, VOCAB = 2560, 6144, 4096, 10240, 26, 8192
+    HQ, HKV, D = 16, 4, 256
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
 
@@ -425,12 +432,30 @@ def decode_step(torch, G, dev, log, M: int = 1) -> dict:
     att = torch.empty(M, ATT, device=dev, dtype=torch.bfloat16)
     mid = torch.empty(M, MLP, device=dev, dtype=torch.bfloat16)
     logits = torch.empty(M, VOCAB, device=dev, dtype=torch.bfloat16)
+    if attn_pos is not None:
+        from breeze_amd import attention as AT
+
+        for L in layers:
+            L["k"] = torch.randn(M, HKV, cache_len, D, device=dev, generator=gen).to(torch.bfloat16)
+            L["v"] = torch.randn(M, HKV, cache_len, D, device=dev, generator=gen).to(torch.bfloat16)
+            L["qn"], L["kn"] = gam(D), gam(D)
+        th = torch.rand(M, D // 2, device=dev, generator=gen) * 6
+        cos = torch.cat([th.cos(), th.cos()], -1).to(torch.bfloat16)
+        sin = torch.cat([th.sin(), th.sin()], -1).to(torch.bfloat16)
+        pos = torch.tensor([attn_pos], device=dev)
+        mask = torch.zeros(M, 1, 1, cache_len, device=dev, dtype=torch.bfloat16)
+        qbuf = torch.empty(M, HQ, D, device=dev)
+        split = AT.default_split(cache_len)
 
     def run():
         hs.copy_(h0)
         for L in layers:
             G.gemv(hs, L["qkv"][0], G.W_INT4_ZP, QKV, sc0=L["qkv"][1], group=GROUP, gamma=L["g1"], eps=EPS, out=qkv)
-            att.copy_(qkv[:, :ATT])
+            if attn_pos is None:
+                att.copy_(qkv[:, :ATT])
+            else:
+                AT.qkv_rope_cache(qkv, cos, sin, pos, L["k"], L["v"], HQ, L["qn"], L["kn"], EPS, qbuf)
+                AT.attn_decode(qbuf, L["k"], L["v"], mask, pos, att, split)
             G.gemv(att, L["o"][0], G.W_INT4_ZP, H, sc0=L["o"][1], group=GROUP, epilogue=G.EPI_RESIDUAL,
                    residual=hs, out=hs)
             G.gemv(hs, L["gu"][0], G.W_INT4_ZP, 2 * MLP, sc0=L["gu"][1], group=GROUP, gamma=L["g2"], eps=EPS,
@@ -439,7 +464,13 @@ def decode_step(torch, G, dev, log, M: int = 1) -> dict:
                    residual=hs, out=hs)
         G.gemv(hs, head, G.W_BF16, VOCAB, gamma=gf, eps=EPS, out=logits)
 
-    nbytes = LAYERS * (algo_bytes(4, QKV, H, M, True, 0) + 2 * 2 * M * ATT + algo_bytes(4, H, ATT, M, False, 2)
+    mid_bytes = 2 * 2 * M * ATT  # the copy: read and write [M, 4096] bf16
+    if attn_pos is not None:
+        # qkv in, q/k norm weights, cos/sin, the new k/v written, keys and values
+        # over [0, pos] read once, the mask row, attention out
+        mid_bytes = (2 * M * QKV + 2 * 2 * D + 2 * 2 * M * D + 2 * 2 * M * HKV * D
+                     + 2 * 2 * M * HKV * (attn_pos + 1) * D + 2 * M * (attn_pos + 1) + 2 * M * ATT)
+    nbytes = LAYERS * (algo_bytes(4, QKV, H, M, True, 0) + mid_bytes + algo_bytes(4, H, ATT, M, False, 2)
                        + algo_bytes(4, 2 * MLP, H, M, True, 1) + algo_bytes(4, H, MLP, M, False, 2)) \
         + algo_bytes(16, VOCAB, H, M, True, 0)
     run()
@@ -463,11 +494,15 @@ def decode_step(torch, G, dev, log, M: int = 1) -> dict:
     torch.cuda.synchronize()
     us = s_ev.elapsed_time(e_ev) * 1e3 / reps
     roof = nbytes / HBM_PEAK_GBPS / 1e3
-    log(f"decode step (26 layers + head, M={M}): {us:.1f} us, roofline {roof:.1f} us ({us / roof:.2f}x)")
+    what = "copy for attention" if attn_pos is None else f"attention at position {attn_pos} of {cache_len}"
+    log(f"decode step (26 layers + head, M={M}, {what}): {us:.1f} us, roofline {roof:.1f} us ({us / roof:.2f}x)")
     del g, layers, head
     torch.cuda.empty_cache()
-    return {"us": round(us, 2), "algorithmic_bytes": nbytes, "roofline_us": round(roof, 2),
-            "x_roofline": round(us / roof, 3), "M": M}
+    res = {"us": round(us, 2), "algorithmic_bytes": nbytes, "roofline_us": round(roof, 2),
+           "x_roofline": round(us / roof, 3), "M": M}
+    if attn_pos is not None:
+        res.update(attn_pos=attn_pos, cache_len=cache_len)
+    return res
 
 
 if __name__ == "__main__":

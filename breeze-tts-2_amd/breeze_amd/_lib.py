@@ -38,6 +38,7 @@ EXPORTS = (
     "bz_dequant",
     "bz_qkv_rope_cache",
     "bz_attn_decode",
+    "bz_attn_step",
     "bz_attn_workspace",
     "bz_attn_default_split",
 )
@@ -109,8 +110,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.bz_attn_decode.restype = ctypes.c_int
     lib.bz_attn_decode.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, i32, i64, vp, f32, i32, vp, vp, i64,
                                    vp]
+    lib.bz_attn_step.restype = ctypes.c_int
+    lib.bz_attn_step.argtypes = [vp, i64, i32, i32, i32, i32, vp, vp, f32, vp, vp, i32, i64, vp, vp, vp, i32, i32, vp,
+                                 vp, i32, i64, f32, i32, vp, vp, i64, vp]
     lib.bz_attn_workspace.restype = ctypes.c_size_t
-    lib.bz_attn_workspace.argtypes = [i32, i32, i32, i32]
+    lib.bz_attn_workspace.argtypes = [i32, i32, i32, i32, i32]
     lib.bz_attn_default_split.restype = ctypes.c_int32
     lib.bz_attn_default_split.argtypes = [i32]
 

@@ -1,9 +1,10 @@
 """torch-facing wrappers of the decode attention C ABI (include/bz_attn.h).
 
-``qkv_rope_cache`` and ``attn_decode`` hand raw device pointers and torch's
-current HIP stream to libbzgemv.so; nothing here computes on the CPU and
-there is no fallback.  ``attention_step`` (models/fused/kernels.py:505-536)
-composes them the way the reference's fused layer calls it.
+``qkv_rope_cache``, ``attn_decode`` and ``attention_step`` hand raw device
+pointers and torch's current HIP stream to libbzgemv.so; nothing here
+computes on the CPU and there is no fallback.  ``attention_step``
+(models/fused/kernels.py:505-536) is one launch of bz_attn_step; the other two
+mirror the reference's separate rope/cache and attention kernels.
 """
 
 from __future__ import annotations
@@ -51,8 +52,8 @@ def default_split(S: int) -> int:
     return int(_lib.lib().bz_attn_default_split(S))
 
 
-def attn_workspace_bytes(B: int, HQ: int, D: int, split: int) -> int:
-    return int(_lib.lib().bz_attn_workspace(B, HQ, D, split))
+def attn_workspace_bytes(B: int, HQ: int, HKV: int, D: int, split: int) -> int:
+    return int(_lib.lib().bz_attn_workspace(B, HQ, HKV, D, split))
 
 
 def qkv_rope_cache(qkv, cos, sin, cache_position, keys, values, HQ: int, q_norm_w=None, k_norm_w=None,
@@ -107,19 +108,23 @@ def qkv_rope_cache(qkv, cos, sin, cache_position, keys, values, HQ: int, q_norm_
     return q_buf
 
 
-_ATTN_PART: dict[tuple, torch.Tensor] = {}
+_ATTN_WS: dict[tuple, torch.Tensor] = {}
 
 
-def _attn_partials(B, HQ, D, split, device) -> Optional[torch.Tensor]:
-    """Split partials [B, HQ, split, D + 2] fp32, one buffer per shape and
-    device (models/fused/kernels.py:480-489)."""
+def _attn_workspace(B, HQ, HKV, D, split, device) -> Optional[torch.Tensor]:
+    """Split partials and arrival counters, one zeroed buffer per shape and
+    device, allocated on first use (models/fused/kernels.py:480-489).  The
+    kernel leaves the counters at zero, so the buffer is never cleared again
+    (nothing to record in a captured graph); calls that share it must not
+    overlap, as with the reference's cached partial buffer."""
     if split <= 1:
         return None
-    key = (B, HQ, D, split, str(device))
-    buf = _ATTN_PART.get(key)
+    key = (B, HQ, HKV, D, split, str(device))
+    buf = _ATTN_WS.get(key)
     if buf is None:
-        buf = torch.empty(attn_workspace_bytes(B, HQ, D, split) // 4, device=device, dtype=torch.float32)
-        _ATTN_PART[key] = buf
+        n = -(-attn_workspace_bytes(B, HQ, HKV, D, split) // 4)
+        buf = torch.zeros(n, device=device, dtype=torch.int32)
+        _ATTN_WS[key] = buf
     return buf
 
 
@@ -144,10 +149,18 @@ def _mask_rows(mask: torch.Tensor, B: int, S: int) -> tuple[torch.Tensor, int, i
     raise ValueError(f"mask has {m2.shape[0]} rows for a batch of {B}")
 
 
+def _out_buffer(out, B, HQ, D, dev):
+    if out is None:
+        return torch.empty(B, HQ * D, device=dev, dtype=torch.bfloat16)
+    if out.dtype != torch.bfloat16 or out.shape != (B, HQ * D) or out.stride(1) != 1:
+        raise ValueError("out must be a bf16 [B, HQ * D] row-major tensor")
+    return out
+
+
 def attn_decode(q, keys, values, mask, cache_position, out=None, split: Optional[int] = None,
                 scale: Optional[float] = None) -> torch.Tensor:
     """softmax(q k^T * scale + mask) v over cache positions [0, pos]; q fp32
-    [B, HQ, D] -> bf16 [B, HQ * D] (kernels.py:404-475)."""
+    [B, HQ, D] -> bf16 [B, HQ * D] (kernels.py:404-475), one launch."""
     dev = q.device
     for n, t in (("keys", keys), ("values", values), ("mask", mask), ("cache_position", cache_position)):
         _gpu(n, t, dev)
@@ -156,18 +169,14 @@ def attn_decode(q, keys, values, mask, cache_position, out=None, split: Optional
     if q.dtype != torch.float32 or not q.is_contiguous():
         raise ValueError("q must be a contiguous float32 [B, HQ, D] tensor")
     m2, mcode, ld_mask = _mask_rows(mask, B, S)
-    if split is None:
-        split = default_split(S)
-    part = _attn_partials(B, HQ, D, split, dev)
-    if out is None:
-        out = torch.empty(B, HQ * D, device=dev, dtype=torch.bfloat16)
-    elif out.dtype != torch.bfloat16 or out.shape != (B, HQ * D) or out.stride(1) != 1:
-        raise ValueError("out must be a bf16 [B, HQ * D] row-major tensor")
+    split = default_split(S) if split is None else split
+    ws = _attn_workspace(B, HQ, HKV, D, split, dev)
+    out = _out_buffer(out, B, HQ, D, dev)
     _lib.check(
         _lib.lib().bz_attn_decode(
             q.data_ptr(), keys.data_ptr(), values.data_ptr(), _dtype_code("keys", keys), B, HQ, HKV, D, S,
             m2.data_ptr(), mcode, ld_mask, cache_position.data_ptr(), D ** -0.5 if scale is None else scale, split,
-            None if part is None else part.data_ptr(), out.data_ptr(), out.stride(0), _lib.stream_of(q)),
+            None if ws is None else ws.data_ptr(), out.data_ptr(), out.stride(0), _lib.stream_of(q)),
         "bz_attn_decode",
     )
     return out
@@ -177,10 +186,55 @@ def attention_step(qkv, cos, sin, cache_position, keys, values, mask, q_norm_w=N
                    out=None, q_buf=None, *, split: Optional[int] = None, seq_len: Optional[torch.Tensor] = None):
     """qkv (B, (HQ + 2 HKV) D) bf16 -> attention output (B, HQ D) bf16, with the
     new k/v written into the static cache (B, HKV, S, D) at cache_position
-    (models/fused/kernels.py:505-536).  Two launches (three with split > 1)."""
-    _, HKV, _, D = keys.shape
+    (models/fused/kernels.py:505-536).  One launch (bz_attn_step): q/k norm,
+    RoPE, the cache write and split attention with its combine.  ``q_buf`` is
+    accepted for the reference's signature and unused (q stays on chip)."""
+    dev = qkv.device
+    for n, t in (("qkv", qkv), ("cos", cos), ("sin", sin), ("cache_position", cache_position), ("keys", keys),
+                 ("values", values), ("mask", mask)):
+        _gpu(n, t, dev)
+    B = qkv.shape[0]
+    _, HKV, S, D = keys.shape
     HQ = (qkv.shape[1] - 2 * HKV * D) // D
     if HQ < 1 or (HQ + 2 * HKV) * D != qkv.shape[1]:
         raise ValueError(f"qkv width {qkv.shape[1]} does not split into q/k/v heads of {D} with {HKV} kv heads")
-    q = qkv_rope_cache(qkv, cos, sin, cache_position, keys, values, HQ, q_norm_w, k_norm_w, eps, q_buf, seq_len)
-    return attn_decode(q, keys, values, mask, cache_position, out, split)
+    if values.shape != keys.shape or values.dtype != keys.dtype:
+        raise ValueError("keys and values must have the same shape and dtype")
+    if not (keys.is_contiguous() and values.is_contiguous()) or keys.shape[0] != B:
+        raise ValueError("the KV cache must be contiguous [B, HKV, S, D] with the batch of qkv")
+    if qkv.dtype != torch.bfloat16:
+        raise TypeError("qkv must be bfloat16")
+    if qkv.stride(1) != 1:
+        qkv = qkv.contiguous()
+    if cache_position.dtype != torch.int64:
+        raise TypeError("cache_position must be int64")
+    if (q_norm_w is None) != (k_norm_w is None):
+        raise ValueError("q_norm_w and k_norm_w come together")
+    cos2, ld_cs = _rows(cos, B, "cos")
+    sin2, ld_sin = _rows(sin, B, "sin")
+    if ld_cs != ld_sin or cos2.dtype != sin2.dtype or cos2.shape[1] != D or sin2.shape[1] != D:
+        raise ValueError("cos and sin must share shape, layout and dtype, with D columns")
+    qn = kn = None
+    if q_norm_w is not None:
+        qn = q_norm_w.to(torch.bfloat16).contiguous()
+        kn = k_norm_w.to(torch.bfloat16).contiguous()
+    if seq_len is not None:
+        _gpu("seq_len", seq_len, dev)
+        if seq_len.dtype != torch.int64 or seq_len.numel() != 1:
+            raise ValueError("seq_len must be a device int64 scalar")
+        if seq_len.data_ptr() == cache_position.data_ptr():
+            raise ValueError("seq_len must not alias cache_position")
+    m2, mcode, ld_mask = _mask_rows(mask, B, S)
+    split = default_split(S) if split is None else split
+    ws = _attn_workspace(B, HQ, HKV, D, split, dev)
+    out = _out_buffer(out, B, HQ, D, dev)
+    _lib.check(
+        _lib.lib().bz_attn_step(
+            qkv.data_ptr(), qkv.stride(0), B, HQ, HKV, D, None if qn is None else qn.data_ptr(),
+            None if kn is None else kn.data_ptr(), eps, cos2.data_ptr(), sin2.data_ptr(), _dtype_code("cos", cos2),
+            ld_cs, cache_position.data_ptr(), keys.data_ptr(), values.data_ptr(), S, _dtype_code("keys", keys),
+            None if seq_len is None else seq_len.data_ptr(), m2.data_ptr(), mcode, ld_mask, D ** -0.5, split,
+            None if ws is None else ws.data_ptr(), out.data_ptr(), out.stride(0), _lib.stream_of(qkv)),
+        "bz_attn_step",
+    )
+    return out

@@ -13,7 +13,7 @@
 // stride ld_cs, 0 to broadcast one row); mask [B][ld_mask] additive bf16 or
 // fp32, or bool (ld_mask 0: one row for all);
 // q_out fp32 [B][HQ][D]; out bf16 [B][ld_out] with q head h at columns
-// h*D..h*D+D-1.  Partials (split > 1) fp32 [B][HQ][split][D + 2] = (acc, m, l).
+// h*D..h*D+D-1.  Partials (split > 1) fp32 [B][HQ][split][D + 4] = (acc, m, l).
 //
 // attn_decode runs one workgroup per (batch row, kv head, split), so the G =
 // HQ/HKV query heads sharing a kv head read its keys and values once.  Its
@@ -44,11 +44,22 @@ __device__ __forceinline__ float ld_any(const void* p, bool f32, int64_t i) {
     return f32 ? reinterpret_cast<const float*>(p)[i] : bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
 }
 
-// Additive mask value: bf16, fp32, or a bool mask (nonzero = attend -> 0,
-// zero -> -1e30, the reference's conversion).
-__device__ __forceinline__ float ld_mask(const void* p, int dtype, int64_t i) {
-    if (dtype == BZ_MASK_BOOL) return reinterpret_cast<const uint8_t*>(p)[i] ? 0.0f : -1e30f;
-    return ld_any(p, dtype == BZ_DT_F32, i);
+// Raw bits of element i of a bf16 (BZ_DT_BF16), fp32 (BZ_DT_F32) or bool
+// (BZ_MASK_BOOL) array, widened later by raw_f32: keeping the conversion
+// away from the load lets the loads issued before and after it stay in
+// flight.
+__device__ __forceinline__ uint32_t ld_raw(const void* p, int kind, int64_t i) {
+    if (kind == BZ_DT_F32) return reinterpret_cast<const uint32_t*>(p)[i];
+    if (kind == BZ_MASK_BOOL) return reinterpret_cast<const uint8_t*>(p)[i];
+    return reinterpret_cast<const uint16_t*>(p)[i];
+}
+
+// bf16 / fp32 as a value; a bool mask entry as additive (nonzero = attend
+// -> 0, zero -> -1e30, the reference's conversion).
+__device__ __forceinline__ float raw_f32(uint32_t v, int kind) {
+    if (kind == BZ_DT_F32) return __uint_as_float(v);
+    if (kind == BZ_MASK_BOOL) return v ? 0.0f : -1e30f;
+    return __uint_as_float(v << 16);
 }
 
 __device__ __forceinline__ void st_any(void* p, bool f32, int64_t i, float v) {
@@ -68,6 +79,23 @@ __device__ __forceinline__ void split8(const float (&v)[8], u32x4& hi, u32x4& lo
     }
     hi = u32x4{h[0], h[1], h[2], h[3]};
     lo = u32x4{l[0], l[1], l[2], l[3]};
+}
+
+// Sum over the 64 lanes, every lane gets it: each 16-lane row by DPP, then
+// rows 0..3 in order (the same order in every kernel of this file).
+__device__ __forceinline__ float row_sum16(float v) {
+    v += dpp_f32<kDppXor1>(v);
+    v += dpp_f32<kDppXor2>(v);
+    v += dpp_f32<0x124>(v);  // row_ror:4
+    return v + dpp_f32<0x128>(v);  // row_ror:8
+}
+
+__device__ __forceinline__ float wave_sum64(float v) {
+    v = row_sum16(v);
+    const int bits = __float_as_int(v);
+    return ((__int_as_float(__builtin_amdgcn_readlane(bits, 0)) + __int_as_float(__builtin_amdgcn_readlane(bits, 16))) +
+            __int_as_float(__builtin_amdgcn_readlane(bits, 32))) +
+           __int_as_float(__builtin_amdgcn_readlane(bits, 48));
 }
 
 // ---------------------------------------------------------------------------
@@ -93,7 +121,7 @@ __global__ void __launch_bounds__(kRopeThreads) qkv_rope_cache_kernel(
         vals[d] = v;
         ss += v * v;
     }
-    ss = wave_sum(ss);
+    ss = wave_sum64(ss);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
     __syncthreads();
     float inv = 1.0f;
@@ -129,26 +157,54 @@ __global__ void __launch_bounds__(kRopeThreads) qkv_rope_cache_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Decode attention.
+// Decode attention: one workgroup per (batch row b, kv head j, split sp).
 // ---------------------------------------------------------------------------
 constexpr int kAttnWaves = 4;
+constexpr int kAttnThreads = 64 * kAttnWaves;
 constexpr int kBlk = 16;           // positions per block (the MFMA's 16 columns)
 constexpr float kNegBig = -1e30f;  // initial running max, as the reference
 constexpr float kLog2e = 1.4426950408889634f;
 
+// 2^x with the hardware instruction alone (results below 2^-126 flush to
+// zero, which a softmax weight can afford).
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 struct AttnParams {
+    // fused step: the token's qkv row and the q/k norm + RoPE inputs
+    const uint16_t* qkv;
+    int64_t ld_qkv;
+    const uint16_t* qn;
+    const uint16_t* kn;
+    float eps;
+    const void* cosp;
+    const void* sinp;
+    int cs_f32;
+    int64_t ld_cs;
+    int64_t* seq_len;
+    // attention only: q already normed and rotated, fp32 [B][HQ][D]
     const float* q;
-    const void* kc;
-    const void* vc;
+    void* kc;
+    void* vc;
     const void* mask;
     int64_t ld_mask;
     int mask_dtype;
     const int64_t* pos;
     float scale;
     int HQ, HKV, G, S, split;
-    float* part;
+    float* part;         // [B][HQ][split][D + 4] (acc, m, l, 2 pad)
+    unsigned* counters;  // [B][HKV] arrivals, zero between calls
     uint16_t* out;
     int64_t ld_out;
+};
+
+// The registers of one 16-position block: key operands and raw value words.
+template <int DL, bool F32C>
+struct KvBlock {
+    static constexpr int T = 2 * DL;                                // MFMA k-steps per key row
+    static constexpr int VW = F32C ? DL : (DL >= 2 ? DL / 2 : 1);   // value words per lane and row
+    u32x4 kh[T], kl[T];
+    uint32_t v[kBlk][VW];
+    uint32_t mraw;  // raw mask entry at this lane's key position
 };
 
 // 8 cache elements of one key row as an MFMA operand; an fp32 cache gives
@@ -167,96 +223,250 @@ __device__ __forceinline__ void load_k8(const void* kc, int64_t off, u32x4& hi, 
     }
 }
 
-// DL consecutive value elements of one row, widened to fp32.
+// DL consecutive value elements of one row, as raw words.
 template <int DL, bool F32C>
-__device__ __forceinline__ void load_v(const void* vc, int64_t off, float (&v)[DL]) {
+__device__ __forceinline__ void load_vraw(const void* vc, int64_t off, uint32_t (&w)[KvBlock<DL, F32C>::VW]) {
     if constexpr (F32C) {
-        const float* p = reinterpret_cast<const float*>(vc) + off;
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(vc) + off;
         if constexpr (DL >= 4) {
             for (int i = 0; i < DL; i += 4) {
-                const float4 t = *reinterpret_cast<const float4*>(p + i);
-                v[i] = t.x;
-                v[i + 1] = t.y;
-                v[i + 2] = t.z;
-                v[i + 3] = t.w;
+                const u32x4 t = *reinterpret_cast<const u32x4*>(p + i);
+                w[i] = t[0];
+                w[i + 1] = t[1];
+                w[i + 2] = t[2];
+                w[i + 3] = t[3];
             }
         } else {
-            for (int i = 0; i < DL; ++i) v[i] = p[i];
+            for (int i = 0; i < DL; ++i) w[i] = p[i];
         }
     } else {
         const uint16_t* p = reinterpret_cast<const uint16_t*>(vc) + off;
         if constexpr (DL == 8) {
             const u32x4 t = *reinterpret_cast<const u32x4*>(p);
-            for (int i = 0; i < 4; ++i) {
-                v[2 * i] = bf16_lo(t[i]);
-                v[2 * i + 1] = bf16_hi(t[i]);
-            }
+            for (int i = 0; i < 4; ++i) w[i] = t[i];
         } else if constexpr (DL == 4) {
             const uint2 t = *reinterpret_cast<const uint2*>(p);
-            v[0] = bf16_lo(t.x);
-            v[1] = bf16_hi(t.x);
-            v[2] = bf16_lo(t.y);
-            v[3] = bf16_hi(t.y);
+            w[0] = t.x;
+            w[1] = t.y;
         } else if constexpr (DL == 2) {
-            const uint32_t t = *reinterpret_cast<const uint32_t*>(p);
-            v[0] = bf16_lo(t);
-            v[1] = bf16_hi(t);
+            w[0] = *reinterpret_cast<const uint32_t*>(p);
         } else {
-            v[0] = bf16_to_f32(p[0]);
+            w[0] = p[0];
         }
     }
 }
 
-// Max / sum over each aligned group of 16 lanes (every lane gets it).
+template <int DL, bool F32C>
+__device__ __forceinline__ float vword(const uint32_t (&w)[KvBlock<DL, F32C>::VW], int e) {
+    if constexpr (F32C) return __uint_as_float(w[e]);
+    if constexpr (DL == 1) return bf16_lo(w[0]);
+    return (e & 1) ? bf16_hi(w[e >> 1]) : bf16_lo(w[e >> 1]);
+}
+
+// One block's loads: key rows s0 + col (lane col), value rows s0 .. s0 + 15
+// and the mask entries, rows past the split's last one clamped to it.  s0
+// and s_hi are wave-uniform, so the value rows' addresses are scalar and
+// each load carries only the lane's column offset.
+template <int DL, bool F32C>
+__device__ __forceinline__ void load_block(const AttnParams& a, int64_t kv_base, int s0, int s_hi, int64_t mrow,
+                                           int lane, KvBlock<DL, F32C>& blk) {
+    constexpr int D = 64 * DL;
+    constexpr int ES = F32C ? 4 : 2;  // element bytes
+    const int last = s_hi - 1;
+    const int col = lane & 15, grp = lane >> 4;
+    const int kpos = min(s0 + col, last);
+    blk.mraw = ld_raw(a.mask, a.mask_dtype, mrow + kpos);  // first: its load depends on the dtype
+    const char* kc = static_cast<const char*>(a.kc) + kv_base * ES;
+    const char* krow = kc + (int64_t)kpos * (D * ES) + 8 * grp * ES;
+    for (int t = 0; t < KvBlock<DL, F32C>::T; ++t) load_k8<F32C>(krow, 32 * t, blk.kh[t], blk.kl[t]);
+    const char* vc = static_cast<const char*>(a.vc) + kv_base * ES;
+    for (int p = 0; p < kBlk; ++p) {
+        const int row = min(s0 + p, last);
+        load_vraw<DL, F32C>(vc + (int64_t)row * (D * ES), DL * lane, blk.v[p]);
+    }
+}
+
+// Max / sum over each aligned group of 16 lanes (one DPP row; every lane
+// gets it): swap within pairs, within quads, then rotate the row by 4 and 8.
+constexpr int kDppRowRor4 = 0x124, kDppRowRor8 = 0x128;
+
 __device__ __forceinline__ float max16(float v) {
-    for (int o = 1; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = fmaxf(v, dpp_f32<kDppXor1>(v));
+    v = fmaxf(v, dpp_f32<kDppXor2>(v));
+    v = fmaxf(v, dpp_f32<kDppRowRor4>(v));
+    return fmaxf(v, dpp_f32<kDppRowRor8>(v));
 }
 
 __device__ __forceinline__ float sum16(float v) {
-    for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += dpp_f32<kDppXor1>(v);
+    v += dpp_f32<kDppXor2>(v);
+    v += dpp_f32<kDppRowRor4>(v);
+    return v + dpp_f32<kDppRowRor8>(v);
 }
 
 __device__ __forceinline__ float bcast(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-// DL = D / 64 columns per lane; GM = 4 or 16 heads of register state (G <= GM).
-template <int DL, int GM, bool F32C>
-__global__ void __launch_bounds__(64 * kAttnWaves) attn_decode_kernel(AttnParams a) {
+// DL = D / 64 columns per lane; GM = 4 or 16 heads of register state (G <=
+// GM); F32C: fp32 cache; FUSED: q (and the new k, v) computed from qkv.
+template <int DL, int GM, bool F32C, bool FUSED>
+__global__ void __launch_bounds__(kAttnThreads) attn_kernel(AttnParams a) {
     constexpr int D = 64 * DL;
-    constexpr int T = D / 32;  // MFMA k-steps per key row
+    constexpr int T = D / 32;
+    constexpr bool PF = !F32C && DL <= 4;  // prefetch the next block (registers allow it)
+    using Blk = KvBlock<DL, F32C>;
+    __shared__ float qf[GM][D];
+    __shared__ float css[(GM + 2) * DL];
+    __shared__ float rinv[GM + 1];
+    __shared__ u32x4 qop[T][2][64];  // the A operand (q hi, lo) of every lane
     __shared__ float p_lds[kAttnWaves][kBlk][GM];
     __shared__ float st_m[kAttnWaves][GM], st_l[kAttnWaves][GM];
-    __shared__ float st_acc[kAttnWaves][GM][D];
+    __shared__ float wgt[kAttnWaves][GM], hm[GM], hl[GM];
+    __shared__ float wsp[GM][BZ_ATTN_MAX_SPLIT];
+    __shared__ float st_acc[kAttnWaves][GM][D];  // also the raw qkv rows of the prologue
+    __shared__ int last;
 
     const int b = blockIdx.x, j = blockIdx.y, sp = blockIdx.z;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: block starts are scalar
     const int G = a.G;
     const int col = lane & 15, grp = lane >> 4;
+
+    // The query rows (FUSED: the token's q heads j*G.., its key head j and
+    // value head j) go out first, as raw words, one element per thread and
+    // row chunk; nothing here waits on the cache position.
+    constexpr int NR = FUSED ? GM + 2 : GM;                            // rows at most
+    constexpr int NI = (NR * D + kAttnThreads - 1) / kAttnThreads;     // elements per thread
+    const int nrows = FUSED ? G + 2 : G;
+    uint32_t pre[NI];
+    // (every thread issues all NI loads, rows past the last clamped to it,
+    // so the number of loads in flight never depends on a branch)
+    for (int i = 0; i < NI; ++i) {
+        const int e = tid + i * kAttnThreads;
+        const int r = min(e / D, nrows - 1), d = e % D;
+        if constexpr (FUSED) {
+            const int head = r < G ? j * G + r : (r == G ? a.HQ + j : a.HQ + a.HKV + j);
+            pre[i] = a.qkv[(int64_t)b * a.ld_qkv + (int64_t)head * D + d];
+        } else {
+            pre[i] = __float_as_uint(a.q[((int64_t)b * a.HQ + (int64_t)j * G + r) * D + d]);
+        }
+    }
+
+    // RoPE and norm operands of this thread's columns: element e = tid +
+    // 256 i of a row sits in column (tid + 256 i) % D, i.e. column tid % D
+    // for D <= 256 and tid or tid + 256 (i even / odd) for D = 512.
+    constexpr int NC = D > kAttnThreads ? 2 : 1;
+    const int cs_kind = a.cs_f32 ? BZ_DT_F32 : BZ_DT_BF16;
+    uint32_t cs_r[NC], sn_r[NC], nw_r[NC][4];  // cos, sin, q/k norm weights at d and its partner
+    if constexpr (FUSED) {
+        const int64_t cs = (int64_t)b * a.ld_cs;
+        for (int c = 0; c < NC; ++c) {
+            const int d = (tid + c * kAttnThreads) % D;
+            const int dp = d < D / 2 ? d + D / 2 : d - D / 2;
+            cs_r[c] = ld_raw(a.cosp, cs_kind, cs + d);
+            sn_r[c] = ld_raw(a.sinp, cs_kind, cs + d);
+            // without norm weights, in-bounds loads of cos stand in (unused)
+            const uint16_t* qn = a.qn ? a.qn : static_cast<const uint16_t*>(a.cosp);
+            const uint16_t* kn = a.qn ? a.kn : static_cast<const uint16_t*>(a.cosp);
+            nw_r[c][0] = qn[d];
+            nw_r[c][1] = qn[dp];
+            nw_r[c][2] = kn[d];
+            nw_r[c][3] = kn[dp];
+        }
+    }
+
     // cache positions [0, min(pos, S - 1)]; none for pos < 0 (output 0)
     const int64_t pos = *a.pos;
     const int kv_len = pos < 0 ? 0 : (pos >= a.S ? a.S : (int)pos + 1);
     const int per = (kv_len + a.split - 1) / a.split;
     const int s_lo = sp * per, s_hi = min(s_lo + per, kv_len);
+    const bool has_new = FUSED && pos >= s_lo && pos < s_hi;  // this split holds the new token
     const int64_t kv_base = ((int64_t)b * a.HKV + j) * a.S * D;
+    const int64_t mrow = (int64_t)b * a.ld_mask;
 
-    // A operand: row `col` = query head j*G + col (zero rows from G on);
-    // element e of step t is scale * q[32t + 8 grp + e].
-    u32x4 qh[T], ql[T];
-    {
-        const bool qv = col < G;
-        const float* qrow = a.q + ((int64_t)b * a.HQ + (int64_t)j * G + (qv ? col : 0)) * D;
-        const float sc = qv ? a.scale : 0.0f;
-        for (int t = 0; t < T; ++t) {
-            const float4 x0 = *reinterpret_cast<const float4*>(qrow + 32 * t + 8 * grp);
-            const float4 x1 = *reinterpret_cast<const float4*>(qrow + 32 * t + 8 * grp + 4);
-            const float v[8] = {x0.x * sc, x0.y * sc, x0.z * sc, x0.w * sc,
-                                x1.x * sc, x1.y * sc, x1.z * sc, x1.w * sc};
-            split8(v, qh[t], ql[t]);
+    // The wave's first block goes out before the prologue's arithmetic --
+    // except in the workgroup whose split holds the new token, which loads
+    // after writing that token's key and value (the barrier at the end of
+    // the prologue orders its own stores before its loads).
+    Blk cur;
+    int s0 = s_lo + wave * kBlk;
+    if (!has_new && s0 < s_hi) load_block<DL, F32C>(a, kv_base, s0, s_hi, mrow, lane, cur);
+
+    if constexpr (FUSED) {
+        // raw rows: [0, G) query heads, G: key head j, G + 1: value head j;
+        // each wave's 64 elements of one i share a row
+        float* raw = &st_acc[0][0][0];
+        for (int i = 0; i < NI; ++i) {
+            const int e = tid + i * kAttnThreads;
+            if (e / D < nrows) {
+                const float v = bf16_to_f32((uint16_t)pre[i]);
+                raw[e] = v;
+                const float ss = wave_sum64(v * v);
+                if (lane == 0) css[e >> 6] = ss;
+            }
+        }
+        __syncthreads();
+        // inverse RMS of each normed row (q heads and the key head), chunk
+        // partials summed in column order
+        if (tid <= G) {
+            float ss = 0.0f;
+            for (int q = 0; q < DL; ++q) ss += css[tid * DL + q];
+            rinv[tid] = a.qn ? 1.0f / sqrtf(ss / (float)D + a.eps) : 1.0f;
+        }
+        __syncthreads();
+        const int nout = G + (has_new ? 1 : 0);
+        for (int i = 0; i < NI; ++i) {
+            const int e = tid + i * kAttnThreads;
+            const int r = e / D, d = e - r * D;
+            if (r >= nout) continue;
+            const int c = NC == 2 ? (i & 1) : 0;
+            const int dp = d < D / 2 ? d + D / 2 : d - D / 2;
+            float v = raw[r * D + d], rr = raw[r * D + dp];
+            if (a.qn) {
+                const float inv = rinv[r];
+                const bool isq = r < G;  // selects, not a run-time index into a register array
+                v = v * inv * bf16_to_f32((uint16_t)(isq ? nw_r[c][0] : nw_r[c][2]));
+                rr = rr * inv * bf16_to_f32((uint16_t)(isq ? nw_r[c][1] : nw_r[c][3]));
+            }
+            if (d < D / 2) rr = -rr;
+            const float o = v * raw_f32(cs_r[c], cs_kind) + rr * raw_f32(sn_r[c], cs_kind);
+            if (r < G) {
+                qf[r][d] = o;
+            } else {  // the new key into the cache
+                st_any(a.kc, F32C, kv_base + pos * D + d, o);
+            }
+        }
+        if (has_new) {
+            for (int d = tid; d < D; d += kAttnThreads) st_any(a.vc, F32C, kv_base + pos * D + d, raw[(G + 1) * D + d]);
+        }
+        if (a.seq_len && b == 0 && j == 0 && sp == 0 && tid == 0) *a.seq_len = pos + 1;
+    } else {
+        float* qflat = &qf[0][0];
+        for (int i = 0; i < NI; ++i) {
+            const int e = tid + i * kAttnThreads;
+            if (e < G * D) qflat[e] = __uint_as_float(pre[i]);
         }
     }
+    __syncthreads();
+
+    if (has_new && s0 < s_hi) load_block<DL, F32C>(a, kv_base, s0, s_hi, mrow, lane, cur);
+
+    // A operand: row `col` = query head j*G + col (zero rows from G on);
+    // element e of step t is scale * q[32t + 8 grp + e], as bf16 hi + lo.
+    // The operands are the same for every wave: built once into LDS (wave w
+    // builds steps w, w + 4, ...) and read back per block.
+    {
+        const bool qv = col < G;
+        const float sc = qv ? a.scale : 0.0f;
+        const float* qrow = qf[qv ? col : 0];
+        for (int t = wave; t < T; t += kAttnWaves) {
+            float v[8];
+            for (int e = 0; e < 8; ++e) v[e] = qrow[32 * t + 8 * grp + e] * sc;
+            split8(v, qop[t][0][lane], qop[t][1][lane]);
+        }
+    }
+    __syncthreads();
 
     // Score state: lane holds heads 4 grp + r (r < 4) at position col; m is
     // uniform over the 16 lanes of a group, l is this lane's share.
@@ -268,63 +478,79 @@ __global__ void __launch_bounds__(64 * kAttnWaves) attn_decode_kernel(AttnParams
     float acc[GM][DL];
     for (int h = 0; h < GM; ++h)
         for (int e = 0; e < DL; ++e) acc[h][e] = 0.0f;
-    const int64_t mrow = (int64_t)b * a.ld_mask;
 
-    for (int s0 = s_lo + wave * kBlk; s0 < s_hi; s0 += kAttnWaves * kBlk) {
+    // One block: scores on the matrix cores, online softmax, p v on the VALU.
+    auto process = [&](Blk& blk, const int s0) __attribute__((always_inline)) {
         const int kpos = s0 + col;
         const bool valid = kpos < s_hi;
-        const int64_t krow = kv_base + (int64_t)(valid ? kpos : s_lo) * D;
-        u32x4 kh[T], kl[T];
-        for (int t = 0; t < T; ++t) load_k8<F32C>(a.kc, krow + 32 * t + 8 * grp, kh[t], kl[t]);
-        float vv[kBlk][DL];
-        for (int p = 0; p < kBlk; ++p) {
-            const int vp = s0 + p < s_hi ? s0 + p : s_lo;
-            load_v<DL, F32C>(a.vc, kv_base + (int64_t)vp * D + DL * lane, vv[p]);
-        }
-        const float mk = valid ? ld_mask(a.mask, a.mask_dtype, mrow + kpos) : 0.0f;
-
         f32x4_t sc = {0.0f, 0.0f, 0.0f, 0.0f};
         for (int t = 0; t < T; ++t) {
-            sc = mfma16(qh[t], kh[t], sc);
-            sc = mfma16(ql[t], kh[t], sc);
-            if constexpr (F32C) sc = mfma16(qh[t], kl[t], sc);
+            const u32x4 qh = qop[t][0][lane], ql = qop[t][1][lane];
+            sc = mfma16(qh, blk.kh[t], sc);
+            sc = mfma16(ql, blk.kh[t], sc);
+            if constexpr (F32C) sc = mfma16(qh, blk.kl[t], sc);
         }
         float alpha[4];
+        const float mk = valid ? raw_f32(blk.mraw, a.mask_dtype) : 0.0f;
         for (int r = 0; r < 4; ++r) {
             const float s = valid ? sc[r] + mk : kNegBig;
             const float mn = fmaxf(m[r], max16(s));
-            alpha[r] = exp2f((m[r] - mn) * kLog2e);
-            const float pr = valid ? exp2f((s - mn) * kLog2e) : 0.0f;
+            alpha[r] = fexp2((m[r] - mn) * kLog2e);
+            const float pr = valid ? fexp2((s - mn) * kLog2e) : 0.0f;
             l[r] = l[r] * alpha[r] + pr;
             m[r] = mn;
-            const int h = 4 * grp + r;
-            if (h < G) p_lds[wave][col][h] = pr;
+            // every head slot of the block is written (rows past G hold
+            // finite values of zero query rows and are never output)
+            if (4 * grp + r < GM) p_lds[wave][col][4 * grp + r] = pr;
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         // rescale by head h's alpha (lane 16 (h / 4), element h % 4)
         for (int h = 0; h < GM; ++h) {
-            if (h < G) {
-                const float al = bcast(alpha[h & 3], 16 * (h >> 2));
-                for (int e = 0; e < DL; ++e) acc[h][e] *= al;
-            }
+            const float al = bcast(alpha[h & 3], 16 * (h >> 2));
+            for (int e = 0; e < DL; ++e) acc[h][e] *= al;
         }
         for (int p = 0; p < kBlk; ++p) {
-            for (int h = 0; h < GM; ++h) {
-                if (h < G) {
-                    const float pw = p_lds[wave][p][h];
-                    for (int e = 0; e < DL; ++e) acc[h][e] += pw * vv[p][e];
-                }
+            float vv[DL];
+            for (int e = 0; e < DL; ++e) vv[e] = vword<DL, F32C>(blk.v[p], e);
+            float pw[GM];
+            for (int h = 0; h < GM; h += 4) {
+                const float4 t = *reinterpret_cast<const float4*>(&p_lds[wave][p][h]);
+                pw[h] = t.x;
+                pw[h + 1] = t.y;
+                pw[h + 2] = t.z;
+                pw[h + 3] = t.w;
             }
+            for (int h = 0; h < GM; ++h)
+                for (int e = 0; e < DL; ++e) acc[h][e] += pw[h] * vv[e];
         }
         // p_lds is rewritten by this wave's next block
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
+    };
+    constexpr int kStride = kAttnWaves * kBlk;
+    if constexpr (PF) {
+        // two register blocks in turn: the next one loads while this one computes
+        Blk other;
+        for (; s0 < s_hi; s0 += 2 * kStride) {
+            const int s1 = s0 + kStride;
+            if (s1 < s_hi) load_block<DL, F32C>(a, kv_base, s1, s_hi, mrow, lane, other);
+            process(cur, s0);
+            if (s1 >= s_hi) break;
+            if (s1 + kStride < s_hi) load_block<DL, F32C>(a, kv_base, s1 + kStride, s_hi, mrow, lane, cur);
+            process(other, s1);
+        }
+    } else {
+        for (; s0 < s_hi; s0 += kStride) {
+            process(cur, s0);
+            if (s0 + kStride < s_hi) load_block<DL, F32C>(a, kv_base, s0 + kStride, s_hi, mrow, lane, cur);
+        }
     }
 
     // Per-wave state to LDS: head 4 grp + r's m and l (l summed over the
     // group's 16 positions).
+    __syncthreads();  // the prologue's raw rows share st_acc
     for (int r = 0; r < 4; ++r) {
         const float ls = sum16(l[r]);
         const int h = 4 * grp + r;
@@ -339,58 +565,161 @@ __global__ void __launch_bounds__(64 * kAttnWaves) attn_decode_kernel(AttnParams
     __syncthreads();
 
     // Merge the waves in a fixed order; write the output or the partial.
-    for (int i = threadIdx.x; i < G * D; i += 64 * kAttnWaves) {
-        const int h = i / D, d = i - h * D;
+    if (tid < G) {
+        const int h = tid;
         float mt = kNegBig;
         for (int w = 0; w < kAttnWaves; ++w) mt = fmaxf(mt, st_m[w][h]);
-        float lt = 0.0f, at = 0.0f;
+        float lt = 0.0f;
         for (int w = 0; w < kAttnWaves; ++w) {
-            const float f = exp2f((st_m[w][h] - mt) * kLog2e);
+            const float f = fexp2((st_m[w][h] - mt) * kLog2e);
+            wgt[w][h] = f;
             lt += st_l[w][h] * f;
-            at += st_acc[w][h][d] * f;
         }
-        const int hq = j * G + h;
+        hm[h] = mt;
+        hl[h] = lt;
+    }
+    __syncthreads();
+    const int64_t hq0 = (int64_t)b * a.HQ + (int64_t)j * G;
+    for (int i = tid; i < G * D; i += kAttnThreads) {
+        const int h = i / D, d = i - h * D;
+        float at = 0.0f;
+        for (int w = 0; w < kAttnWaves; ++w) at += st_acc[w][h][d] * wgt[w][h];
+        const float lt = hl[h];
         if (a.split == 1) {
-            a.out[(int64_t)b * a.ld_out + (int64_t)hq * D + d] = f32_to_bf16(lt > 0.0f ? at / lt : 0.0f);
-        } else {
-            float* pp = a.part + (((int64_t)b * a.HQ + hq) * a.split + sp) * (D + 2);
-            pp[d] = at;
+            a.out[(int64_t)b * a.ld_out + (int64_t)(j * G + h) * D + d] = f32_to_bf16(lt > 0.0f ? at / lt : 0.0f);
+        } else {  // agent-scope stores: coherent across XCDs without an L2 write-back
+            float* pp = a.part + ((hq0 + h) * a.split + sp) * (D + 4);
+            __hip_atomic_store(&pp[d], at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (d == 0) {
-                pp[D] = mt;
-                pp[D + 1] = lt;
+                __hip_atomic_store(&pp[D], hm[h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&pp[D + 1], lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
     }
-}
+    if (a.split == 1) return;
 
-// One workgroup of 64 lanes per (batch row, q head): merge the splits in
-// split order.
-__global__ void __launch_bounds__(64) attn_combine_kernel(const float* part, uint16_t* out, int64_t ld_out, int HQ,
-                                                          int D, int split) {
-    const int b = blockIdx.x, h = blockIdx.y;
-    const float* base = part + ((int64_t)b * HQ + h) * split * (D + 2);
-    float m = kNegBig;
-    for (int s = 0; s < split; ++s) m = fmaxf(m, base[s * (D + 2) + D]);
-    float l = 0.0f;
-    for (int s = 0; s < split; ++s) l += base[s * (D + 2) + D + 1] * exp2f((base[s * (D + 2) + D] - m) * kLog2e);
-    for (int d = threadIdx.x; d < D; d += 64) {
-        float acc = 0.0f;
-        for (int s = 0; s < split; ++s) acc += base[s * (D + 2) + d] * exp2f((base[s * (D + 2) + D] - m) * kLog2e);
-        out[(int64_t)b * ld_out + (int64_t)h * D + d] = f32_to_bf16(l > 0.0f ? acc / l : 0.0f);
+    // The last workgroup of (b, j) to finish combines the splits.  Every
+    // thread waits until its partial stores have completed (agent-scope
+    // stores complete at the point of coherence) before the workgroup counts
+    // its arrival; the last one reads the partials with agent-scope loads.
+    // No L2 write-back or invalidate is needed for that.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned prev =
+            __hip_atomic_fetch_add(&a.counters[b * a.HKV + j], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = prev == (unsigned)a.split - 1u;
     }
+    __syncthreads();
+    if (!last) return;
+    // Weights first: wave w takes heads w, w + 4, ...; lane s reads split s's
+    // (m, l) and the wave forms w_s = exp(m_s - max m) and sum_s w_s l_s.
+    for (int h = wave; h < G; h += kAttnWaves) {
+        const float* ph = a.part + (hq0 + h) * a.split * (D + 4);
+        const bool in = lane < a.split;
+        const int sl = in ? lane : 0;
+        const float ms0 = __hip_atomic_load(ph + sl * (D + 4) + D, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float ls0 = __hip_atomic_load(ph + sl * (D + 4) + D + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float ms = in ? ms0 : kNegBig;
+        const float mt = wave_max(ms);
+        const float w = in ? fexp2((ms - mt) * kLog2e) : 0.0f;
+        wsp[h][lane] = w;
+        const float lt = wave_sum(in ? ls0 * w : 0.0f);
+        if (lane == 0) hl[h] = lt;
+    }
+    __syncthreads();
+    // Then the columns: element i = (h, d) sums w_s acc_s over the splits in
+    // split order; each thread keeps NE elements x 8 splits of loads in flight.
+    constexpr int NE = (GM * D + kAttnThreads - 1) / kAttnThreads;
+    float acc0[NE];
+    for (int q = 0; q < NE; ++q) acc0[q] = 0.0f;
+    for (int s0 = 0; s0 < a.split; s0 += 8) {
+        float v[NE][8];
+        for (int q = 0; q < NE; ++q) {
+            const int i = min(tid + q * kAttnThreads, G * D - 1);
+            const int h = i / D, d = i - h * D;
+            const float* ph = a.part + (hq0 + h) * a.split * (D + 4) + d;
+            for (int u = 0; u < 8; ++u) {
+                const int sidx = min(s0 + u, a.split - 1);
+                v[q][u] = __hip_atomic_load(ph + sidx * (D + 4), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        for (int q = 0; q < NE; ++q) {
+            const int h = min(tid + q * kAttnThreads, G * D - 1) / D;
+            for (int u = 0; u < 8; ++u)
+                if (s0 + u < a.split) acc0[q] += v[q][u] * wsp[h][s0 + u];
+        }
+    }
+    for (int q = 0; q < NE; ++q) {
+        const int i = tid + q * kAttnThreads;
+        if (i < G * D) {
+            const int h = i / D, d = i - h * D;
+            const float lt = hl[h];
+            a.out[(int64_t)b * a.ld_out + (int64_t)(j * G + h) * D + d] =
+                f32_to_bf16(lt > 0.0f ? acc0[q] / lt : 0.0f);
+        }
+    }
+    if (tid == 0) __hip_atomic_store(&a.counters[b * a.HKV + j], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int DL, int GM>
+template <int DL, int GM, bool FUSED>
 static void launch_attn(const AttnParams& a, bool f32c, dim3 grid, hipStream_t st) {
     if (f32c)
-        hipLaunchKernelGGL((attn_decode_kernel<DL, GM, true>), grid, dim3(64 * kAttnWaves), 0, st, a);
+        hipLaunchKernelGGL((attn_kernel<DL, GM, true, FUSED>), grid, dim3(kAttnThreads), 0, st, a);
     else
-        hipLaunchKernelGGL((attn_decode_kernel<DL, GM, false>), grid, dim3(64 * kAttnWaves), 0, st, a);
+        hipLaunchKernelGGL((attn_kernel<DL, GM, false, FUSED>), grid, dim3(kAttnThreads), 0, st, a);
 }
 
-static int launched() { return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH; }
+template <bool FUSED>
+static int launch_attn_any(const AttnParams& a, int D, bool f32c, dim3 grid, hipStream_t st) {
+    const bool g4 = a.G <= 4;
+    switch (D) {
+        case 64: g4 ? launch_attn<1, 4, FUSED>(a, f32c, grid, st) : launch_attn<1, 16, FUSED>(a, f32c, grid, st); break;
+        case 128: g4 ? launch_attn<2, 4, FUSED>(a, f32c, grid, st) : launch_attn<2, 16, FUSED>(a, f32c, grid, st); break;
+        case 256: g4 ? launch_attn<4, 4, FUSED>(a, f32c, grid, st) : launch_attn<4, 16, FUSED>(a, f32c, grid, st); break;
+        default: launch_attn<8, 4, FUSED>(a, f32c, grid, st); break;
+    }
+    return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
+}
 
 static bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; }
+
+static size_t partial_floats(int B, int HQ, int D, int split) { return (size_t)B * HQ * split * (D + 4); }
+
+// Checks shared by bz_attn_decode and bz_attn_step; fills the attention part
+// of the parameters.
+static int attn_setup(AttnParams& a, const void* k_cache, const void* v_cache, int cache_dtype, int B, int HQ, int HKV,
+                      int D, int S, const void* mask, int mask_dtype, int64_t ld_mask, const int64_t* pos, float scale,
+                      int split, void* workspace, void* out, int64_t ld_out) {
+    if (!k_cache || !v_cache || !mask || !pos || !out) return BZ_ERR_INVALID_ARG;
+    if (B < 1 || HQ < 1 || HKV < 1 || S < 1 || HQ % HKV) return BZ_ERR_INVALID_ARG;
+    if (cache_dtype != BZ_DT_BF16 && cache_dtype != BZ_DT_F32) return BZ_ERR_INVALID_ARG;
+    if (mask_dtype != BZ_DT_BF16 && mask_dtype != BZ_DT_F32 && mask_dtype != BZ_MASK_BOOL) return BZ_ERR_INVALID_ARG;
+    if (split < 1 || split > BZ_ATTN_MAX_SPLIT || (split > 1 && !workspace)) return BZ_ERR_INVALID_ARG;
+    if ((ld_mask != 0 && ld_mask < S) || ld_mask < 0 || ld_out < (int64_t)HQ * D) return BZ_ERR_SHAPE;
+    const int G = HQ / HKV;
+    if (D != 64 && D != 128 && D != 256 && D != 512) return BZ_ERR_UNSUPPORTED;
+    if (G > 16 || (G > 4 && D == 512)) return BZ_ERR_UNSUPPORTED;
+    if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(out, 2) || !aligned(workspace, 4))
+        return BZ_ERR_ALIGNMENT;
+    a.kc = const_cast<void*>(k_cache);
+    a.vc = const_cast<void*>(v_cache);
+    a.mask = mask;
+    a.ld_mask = ld_mask;
+    a.mask_dtype = mask_dtype;
+    a.pos = pos;
+    a.scale = scale;
+    a.HQ = HQ;
+    a.HKV = HKV;
+    a.G = G;
+    a.S = S;
+    a.split = split;
+    a.part = static_cast<float*>(workspace);
+    a.counters = split > 1 ? reinterpret_cast<unsigned*>(a.part + partial_floats(B, HQ, D, split)) : nullptr;
+    a.out = static_cast<uint16_t*>(out);
+    a.ld_out = ld_out;
+    return BZ_OK;
+}
 
 }  // namespace bz
 
@@ -410,7 +739,7 @@ extern "C" int bz_qkv_rope_cache(const void* qkv, int64_t ld_qkv, int32_t B, int
                        static_cast<const uint16_t*>(q_norm), static_cast<const uint16_t*>(k_norm), eps, cos, sin,
                        cs_dtype == BZ_DT_F32, ld_cs, pos, q_out, k_cache, v_cache, S, cache_dtype == BZ_DT_F32,
                        seq_len);
-    return launched();
+    return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }
 
 extern "C" int32_t bz_attn_default_split(int32_t S) {
@@ -418,55 +747,49 @@ extern "C" int32_t bz_attn_default_split(int32_t S) {
     return s < 1 ? 1 : (s > 32 ? 32 : s);
 }
 
-extern "C" size_t bz_attn_workspace(int32_t B, int32_t HQ, int32_t D, int32_t split) {
-    if (B < 1 || HQ < 1 || D < 1 || split <= 1) return 0;
-    return (size_t)B * HQ * split * (D + 2) * sizeof(float);
+extern "C" size_t bz_attn_workspace(int32_t B, int32_t HQ, int32_t HKV, int32_t D, int32_t split) {
+    if (B < 1 || HQ < 1 || HKV < 1 || D < 1 || split <= 1) return 0;
+    return partial_floats(B, HQ, D, split) * sizeof(float) + (size_t)B * HKV * sizeof(unsigned);
 }
 
 extern "C" int bz_attn_decode(const float* q, const void* k_cache, const void* v_cache, int32_t cache_dtype, int32_t B,
                               int32_t HQ, int32_t HKV, int32_t D, int32_t S, const void* mask, int32_t mask_dtype,
-                              int64_t ld_mask, const int64_t* pos, float scale, int32_t split, float* part, void* out, int64_t ld_out,
-                              void* stream) {
-    if (!q || !k_cache || !v_cache || !mask || !pos || !out) return BZ_ERR_INVALID_ARG;
-    if (B < 1 || HQ < 1 || HKV < 1 || S < 1 || HQ % HKV) return BZ_ERR_INVALID_ARG;
-    if (cache_dtype != BZ_DT_BF16 && cache_dtype != BZ_DT_F32) return BZ_ERR_INVALID_ARG;
-    if (split < 1 || split > BZ_ATTN_MAX_SPLIT || (split > 1 && !part)) return BZ_ERR_INVALID_ARG;
-    if (mask_dtype != BZ_DT_BF16 && mask_dtype != BZ_DT_F32 && mask_dtype != BZ_MASK_BOOL) return BZ_ERR_INVALID_ARG;
-    if ((ld_mask != 0 && ld_mask < S) || ld_mask < 0 || ld_out < (int64_t)HQ * D) return BZ_ERR_SHAPE;
-    const int G = HQ / HKV;
-    if (D != 64 && D != 128 && D != 256 && D != 512) return BZ_ERR_UNSUPPORTED;
-    if (G > 16 || (G > 4 && D == 512)) return BZ_ERR_UNSUPPORTED;
-    if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(out, 2)) return BZ_ERR_ALIGNMENT;
-    AttnParams a;
+                              int64_t ld_mask, const int64_t* pos, float scale, int32_t split, void* workspace,
+                              void* out, int64_t ld_out, void* stream) {
+    if (!q) return BZ_ERR_INVALID_ARG;
+    AttnParams a = {};
+    int rc = attn_setup(a, k_cache, v_cache, cache_dtype, B, HQ, HKV, D, S, mask, mask_dtype, ld_mask, pos, scale,
+                        split, workspace, out, ld_out);
+    if (rc != BZ_OK) return rc;
+    if (!aligned(q, 16)) return BZ_ERR_ALIGNMENT;
     a.q = q;
-    a.kc = k_cache;
-    a.vc = v_cache;
-    a.mask = mask;
-    a.ld_mask = ld_mask;
-    a.mask_dtype = mask_dtype;
-    a.pos = pos;
-    a.scale = scale;
-    a.HQ = HQ;
-    a.HKV = HKV;
-    a.G = G;
-    a.S = S;
-    a.split = split;
-    a.part = part;
-    a.out = static_cast<uint16_t*>(out);
-    a.ld_out = ld_out;
-    const bool f32c = cache_dtype == BZ_DT_F32;
-    const dim3 grid(B, HKV, split);
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    const bool g4 = G <= 4;
-    switch (D) {
-        case 64: g4 ? launch_attn<1, 4>(a, f32c, grid, st) : launch_attn<1, 16>(a, f32c, grid, st); break;
-        case 128: g4 ? launch_attn<2, 4>(a, f32c, grid, st) : launch_attn<2, 16>(a, f32c, grid, st); break;
-        case 256: g4 ? launch_attn<4, 4>(a, f32c, grid, st) : launch_attn<4, 16>(a, f32c, grid, st); break;
-        default: launch_attn<8, 4>(a, f32c, grid, st); break;
-    }
-    const int rc = launched();
-    if (rc != BZ_OK || split == 1) return rc;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(B, HQ), dim3(64), 0, st, part, static_cast<uint16_t*>(out), ld_out, HQ,
-                       D, split);
-    return launched();
+    return launch_attn_any<false>(a, D, cache_dtype == BZ_DT_F32, dim3(B, HKV, split),
+                                  static_cast<hipStream_t>(stream));
+}
+
+extern "C" int bz_attn_step(const void* qkv, int64_t ld_qkv, int32_t B, int32_t HQ, int32_t HKV, int32_t D,
+                            const void* q_norm, const void* k_norm, float eps, const void* cos, const void* sin,
+                            int32_t cs_dtype, int64_t ld_cs, const int64_t* pos, void* k_cache, void* v_cache,
+                            int32_t S, int32_t cache_dtype, int64_t* seq_len, const void* mask, int32_t mask_dtype,
+                            int64_t ld_mask, float scale, int32_t split, void* workspace, void* out, int64_t ld_out,
+                            void* stream) {
+    if (!qkv || !cos || !sin || (q_norm == nullptr) != (k_norm == nullptr)) return BZ_ERR_INVALID_ARG;
+    if (cs_dtype != BZ_DT_BF16 && cs_dtype != BZ_DT_F32) return BZ_ERR_INVALID_ARG;
+    AttnParams a = {};
+    int rc = attn_setup(a, k_cache, v_cache, cache_dtype, B, HQ, HKV, D, S, mask, mask_dtype, ld_mask, pos, scale,
+                        split, workspace, out, ld_out);
+    if (rc != BZ_OK) return rc;
+    if (ld_qkv < (int64_t)(HQ + 2 * HKV) * D || ld_cs < 0) return BZ_ERR_SHAPE;
+    a.qkv = static_cast<const uint16_t*>(qkv);
+    a.ld_qkv = ld_qkv;
+    a.qn = static_cast<const uint16_t*>(q_norm);
+    a.kn = static_cast<const uint16_t*>(k_norm);
+    a.eps = eps;
+    a.cosp = cos;
+    a.sinp = sin;
+    a.cs_f32 = cs_dtype == BZ_DT_F32;
+    a.ld_cs = ld_cs;
+    a.seq_len = seq_len;
+    return launch_attn_any<true>(a, D, cache_dtype == BZ_DT_F32, dim3(B, HKV, split),
+                                 static_cast<hipStream_t>(stream));
 }

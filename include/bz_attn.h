@@ -59,23 +59,47 @@ int bz_qkv_rope_cache(const void* qkv, int64_t ld_qkv, int32_t B, int32_t HQ,
                       int64_t* seq_len, void* stream);
 
 /* out = softmax(q k^T * scale + mask) v over cache positions [0, pos], per
- * query head, with query head h reading kv head h / (HQ / HKV).  The
- * positions are cut into `split` equal ranges; split > 1 needs `part`, an
- * fp32 workspace of bz_attn_workspace(B, HQ, D, split) bytes, and adds a
- * combine launch.  Replaces attn_decode_kernel + attn_combine_kernel,
- * models/fused/kernels.py:404-475 (attention_step :528-536 picks split 1
- * for S <= 256, else 8; bz_attn_default_split is this build's choice).
+ * query head, with query head h reading kv head h / (HQ / HKV); q fp32
+ * [B][HQ][D] already normed and rotated.  One launch: a workgroup per
+ * (batch row, kv head, split) with the positions cut into `split` equal
+ * ranges; for split > 1 the last workgroup of each (row, kv head) to finish
+ * combines the ranges, through `workspace` (bz_attn_workspace bytes, zeroed
+ * once before its first use: the kernel leaves its arrival counters at zero
+ * again).  Calls that share a workspace must not overlap.  Replaces
+ * attn_decode_kernel + attn_combine_kernel, models/fused/kernels.py:404-475
+ * (attention_step :528-536 picks split 1 for S <= 256, else 8;
+ * bz_attn_default_split is this build's choice).
  * D in {64, 128, 256, 512}; HQ / HKV <= 16 (<= 4 for D = 512). */
 int bz_attn_decode(const float* q, const void* k_cache, const void* v_cache,
                    int32_t cache_dtype, int32_t B, int32_t HQ, int32_t HKV,
                    int32_t D, int32_t S, const void* mask,
                    int32_t mask_dtype, int64_t ld_mask,
-                   const int64_t* pos, float scale, int32_t split, float* part,
-                   void* out, int64_t ld_out, void* stream);
+                   const int64_t* pos, float scale, int32_t split,
+                   void* workspace, void* out, int64_t ld_out, void* stream);
 
-/* fp32 workspace bytes bz_attn_decode needs (0 for split == 1).  Replaces
- * the partial-buffer cache _attn_partials, models/fused/kernels.py:481-489. */
-size_t bz_attn_workspace(int32_t B, int32_t HQ, int32_t D, int32_t split);
+/* The whole attention step of a decode token in one launch: the work of
+ * bz_qkv_rope_cache (q/k RMSNorm, RoPE, new k and v into the caches at pos,
+ * seq_len = pos + 1 when given; seq_len must not alias pos) and of
+ * bz_attn_decode, with q never leaving the chip and the new token's k and v
+ * taken from the workgroup's own registers.  Replaces attention_step,
+ * models/fused/kernels.py:505-536 (three launches there).  Same limits and
+ * workspace as bz_attn_decode. */
+int bz_attn_step(const void* qkv, int64_t ld_qkv, int32_t B, int32_t HQ,
+                 int32_t HKV, int32_t D, const void* q_norm,
+                 const void* k_norm, float eps, const void* cos,
+                 const void* sin, int32_t cs_dtype, int64_t ld_cs,
+                 const int64_t* pos, void* k_cache, void* v_cache, int32_t S,
+                 int32_t cache_dtype, int64_t* seq_len, const void* mask,
+                 int32_t mask_dtype, int64_t ld_mask, float scale,
+                 int32_t split, void* workspace, void* out, int64_t ld_out,
+                 void* stream);
+
+/* Workspace bytes of bz_attn_decode / bz_attn_step (0 for split == 1): the
+ * fp32 split partials [B][HQ][split][D + 4] and B * HKV arrival counters.
+ * Replaces the partial-buffer cache _attn_partials,
+ * models/fused/kernels.py:481-489. */
+size_t bz_attn_workspace(int32_t B, int32_t HQ, int32_t HKV, int32_t D,
+                         int32_t split);
 
 /* Split count for a static cache of S positions: about 128 positions per
  * workgroup at a full cache, between 1 and 32. */

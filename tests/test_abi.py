@@ -196,7 +196,7 @@ def test_rope_cache_validation(L, kw, status):
 def _attn_args(L, **kw):
     f = 1 << 20
     a = dict(q=f, kc=f, vc=f, cache_dtype=L.DT_BF16, B=2, HQ=16, HKV=4, D=256, S=512, mask=f, mask_dtype=L.DT_BF16,
-             ld_mask=512, pos=f, scale=0.0625, split=4, part=f, out=f, ld_out=4096, stream=None)
+             ld_mask=512, pos=f, scale=0.0625, split=4, ws=f, out=f, ld_out=4096, stream=None)
     a.update(kw)
     return list(a.values())
 
@@ -212,7 +212,8 @@ def _attn_args(L, **kw):
         ({"ld_mask": -1}, "ERR_SHAPE"),
         ({"split": 0}, "ERR_INVALID_ARG"),
         ({"split": 65}, "ERR_INVALID_ARG"),
-        ({"part": None}, "ERR_INVALID_ARG"),             # split > 1 needs the workspace
+        ({"ws": None}, "ERR_INVALID_ARG"),               # split > 1 needs the workspace
+        ({"ws": (1 << 20) + 2}, "ERR_ALIGNMENT"),
         ({"ld_mask": 100}, "ERR_SHAPE"),
         ({"ld_out": 4095}, "ERR_SHAPE"),
         ({"D": 96, "ld_out": 16 * 96}, "ERR_UNSUPPORTED"),
@@ -226,6 +227,34 @@ def test_attn_validation(L, kw, status):
     assert L.lib().bz_attn_decode(*_attn_args(L, **kw)) == getattr(L, status)
 
 
+def _step_args(L, **kw):
+    f = 1 << 20
+    a = dict(qkv=f, ld_qkv=24 * 256, B=2, HQ=16, HKV=4, D=256, qn=f, kn=f, eps=1e-6, cos=f, sin=f,
+             cs_dtype=L.DT_BF16, ld_cs=256, pos=f, kc=f, vc=f, S=512, cache_dtype=L.DT_BF16, seq_len=None, mask=f,
+             mask_dtype=L.DT_BF16, ld_mask=512, scale=0.0625, split=4, ws=f, out=f, ld_out=4096, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize(
+    "kw,status",
+    [
+        ({"qkv": None}, "ERR_INVALID_ARG"),
+        ({"cos": None}, "ERR_INVALID_ARG"),
+        ({"qn": None}, "ERR_INVALID_ARG"),             # q and k norm weights come together
+        ({"cs_dtype": 2}, "ERR_INVALID_ARG"),
+        ({"ld_qkv": 24 * 256 - 8}, "ERR_SHAPE"),
+        ({"ld_cs": -1}, "ERR_SHAPE"),
+        ({"HQ": 15}, "ERR_INVALID_ARG"),
+        ({"ws": None}, "ERR_INVALID_ARG"),
+        ({"D": 96, "ld_qkv": 24 * 96, "ld_out": 16 * 96}, "ERR_UNSUPPORTED"),
+        ({"kc": (1 << 20) + 8}, "ERR_ALIGNMENT"),
+    ],
+)
+def test_attn_step_validation(L, kw, status):
+    assert L.lib().bz_attn_step(*_step_args(L, **kw)) == getattr(L, status)
+
+
 def test_attn_header_constants(L):
     text = HEADERS[1].read_text()
     assert int(re.search(r"#define\s+BZ_MASK_BOOL\s+(\d+)", text).group(1)) == L.MASK_BOOL
@@ -234,8 +263,8 @@ def test_attn_header_constants(L):
 
 def test_attn_workspace_and_split(L):
     lib = L.lib()
-    assert lib.bz_attn_workspace(2, 16, 256, 1) == 0
-    assert lib.bz_attn_workspace(2, 16, 256, 8) == 2 * 16 * 8 * 258 * 4
+    assert lib.bz_attn_workspace(2, 16, 4, 256, 1) == 0
+    assert lib.bz_attn_workspace(2, 16, 4, 256, 8) == 2 * 16 * 8 * 260 * 4 + 2 * 4 * 4
     assert [lib.bz_attn_default_split(s) for s in (1, 128, 129, 1024, 2048, 8192)] == [1, 1, 2, 8, 16, 32]
 
 

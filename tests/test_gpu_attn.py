@@ -174,11 +174,66 @@ def test_attn_position_outside_cache():
     np.testing.assert_array_equal(f32(big), f32(full))
 
 
+@pytest.mark.parametrize("HQ,HKV,D", [(16, 4, 256), (8, 2, 128), (16, 1, 64), (4, 1, 512)])
+@pytest.mark.parametrize("pos,S,split", [(0, 64, 1), (37, 64, 1), (37, 64, 4), (511, 512, None), (300, 512, 16)])
+@pytest.mark.parametrize("qk_norm", [True, False])
+def test_attention_step_fused_matches_oracle_and_unfused(HQ, HKV, D, pos, S, split, qk_norm):
+    """One launch of bz_attn_step against the oracle's rope + cache write +
+    attention, and against qkv_rope_cache + attn_decode (the same arithmetic
+    in two launches: bit-identical for D <= 256, where both sum the head
+    norm in the same order)."""
+    B = 2
+    qkv, keys, values = _case(B, HQ, HKV, D, S, 30 + pos, fill=pos)
+    cos, sin = (O.round_bf16(t) for t in _rope_tables(B, D, 31))   # the tables the GPU gets, as bf16
+    rng = np.random.default_rng(32)
+    qn = O.round_bf16(1 + 0.1 * rng.standard_normal(D).astype(np.float32)) if qk_norm else None
+    kn = O.round_bf16(1 + 0.1 * rng.standard_normal(D).astype(np.float32)) if qk_norm else None
+    allow = rng.random((B, S)) > 0.1
+    allow[:, pos] = True
+    mask = np.where(allow, 0.0, float(torch.finfo(torch.bfloat16).min))
+    mask_t = torch.from_numpy(mask.reshape(B, 1, 1, S)).to(torch.bfloat16).to(DEV)
+    args = (_bf16(cos), _bf16(sin), torch.tensor([pos], device=DEV))
+    nw = (None if qn is None else _bf16(qn), None if kn is None else _bf16(kn))
+    kc, vc = _bf16(keys), _bf16(values)
+    kc2, vc2 = kc.clone(), vc.clone()
+    counter = torch.zeros((), dtype=torch.int64, device=DEV)
+    out = T.attention_step(_bf16(qkv), *args, kc, vc, mask_t, *nw, 1e-6, split=split, seq_len=counter)
+    q = T.qkv_rope_cache(_bf16(qkv), *args, kc2, vc2, HQ, *nw, 1e-6)
+    out2 = T.attn_decode(q, kc2, vc2, mask_t, args[2], split=split)
+    assert int(counter) == pos + 1
+    np.testing.assert_array_equal(f32(kc), f32(kc2))
+    np.testing.assert_array_equal(f32(vc), f32(vc2))
+    if D <= 256:
+        np.testing.assert_array_equal(f32(out), f32(out2))
+    q_ref = A.qkv_rope_cache(qkv, HQ, HKV, D, cos, sin, pos, keys, values, qn, kn, 1e-6)
+    ref = A.attn_decode(q_ref, keys, values, mask, pos)
+    assert O.rel_err(f32(out), ref) <= TIGHT
+    step = 2.0 ** -7
+    np.testing.assert_allclose(f32(kc)[:, :, pos], keys[:, :, pos], rtol=step, atol=1e-6)
+
+
+def test_attention_step_workspace_reuse_across_shapes_and_calls():
+    """Many calls in a row with split > 1 (the arrival counters must return
+    to zero after every call) at changing positions, two batch sizes."""
+    HQ, HKV, D, S = 16, 4, 256, 256
+    for B in (1, 2):
+        qkv, keys, values = _case(B, HQ, HKV, D, S, 40 + B)
+        cos, sin = (O.round_bf16(t) for t in _rope_tables(B, D, 41))
+        mask_t = torch.zeros(B, 1, 1, S, device=DEV)
+        kc, vc = _bf16(keys), _bf16(values)
+        for pos in (255, 3, 100, 0, 200, 255, 17):
+            kref, vref = f32(kc), f32(vc)
+            out = T.attention_step(_bf16(qkv), _bf16(cos), _bf16(sin), torch.tensor([pos], device=DEV), kc, vc,
+                                   mask_t, split=8)
+            q_ref = A.qkv_rope_cache(qkv, HQ, HKV, D, cos, sin, pos, kref, vref)
+            assert O.rel_err(f32(out), A.attn_decode(q_ref, kref, vref, np.zeros((B, S)), pos)) <= TIGHT, (B, pos)
+
+
 def test_attention_step_graph_replays_track_device_position():
     """attention_step captured once in a HIP graph, replayed with the device
     position and mask updated between replays: every replay equals an eager
     call on a cache copy."""
-    B, HQ, HKV, D, S = 2, 16, 4, 256, 96
+    B, HQ, HKV, D, S = 2, 16, 4, 256, 192
     qkv, keys, values = _case(B, HQ, HKV, D, S, 14, fill=0)
     cos, sin = _rope_tables(B, D, 15)
     qkv_t, cos_t, sin_t = _bf16(qkv), _bf16(cos), _bf16(sin)
@@ -201,7 +256,7 @@ def test_attention_step_graph_replays_track_device_position():
             step(kc, vc, out, qbuf)
     torch.cuda.current_stream().wait_stream(st)
     torch.cuda.synchronize()
-    for t in range(0, 90, 7):
+    for t in range(0, 190, 11):
         pos.fill_(t)
         mask[:, :, :, : t + 1] = 0
         qkv_t.copy_(_bf16(np.random.default_rng(t).standard_normal(qkv.shape) * 2))
