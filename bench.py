@@ -444,7 +444,6 @@ def decode_step(torch, G, dev, log, M: int = 1, attn_pos: int | None = None, cac
         sin = torch.cat([th.sin(), th.sin()], -1).to(torch.bfloat16)
         pos = torch.tensor([attn_pos], device=dev)
         mask = torch.zeros(M, 1, 1, cache_len, device=dev, dtype=torch.bfloat16)
-        qbuf = torch.empty(M, HQ, D, device=dev)
         split = AT.default_split(cache_len)
 
     def run():
@@ -454,8 +453,7 @@ def decode_step(torch, G, dev, log, M: int = 1, attn_pos: int | None = None, cac
             if attn_pos is None:
                 att.copy_(qkv[:, :ATT])
             else:
-                AT.qkv_rope_cache(qkv, cos, sin, pos, L["k"], L["v"], HQ, L["qn"], L["kn"], EPS, qbuf)
-                AT.attn_decode(qbuf, L["k"], L["v"], mask, pos, att, split)
+                AT.attention_step(qkv, cos, sin, pos, L["k"], L["v"], mask, L["qn"], L["kn"], EPS, att, split=split)
             G.gemv(att, L["o"][0], G.W_INT4_ZP, H, sc0=L["o"][1], group=GROUP, epilogue=G.EPI_RESIDUAL,
                    residual=hs, out=hs)
             G.gemv(hs, L["gu"][0], G.W_INT4_ZP, 2 * MLP, sc0=L["gu"][1], group=GROUP, gamma=L["g2"], eps=EPS,
