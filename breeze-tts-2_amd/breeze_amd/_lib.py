@@ -36,6 +36,7 @@ EXPORTS = (
     "bz_quantize_int4",
     "bz_quantize_fp8",
     "bz_dequant",
+    "bz_head_f32",
     "bz_qkv_rope_cache",
     "bz_attn_decode",
     "bz_attn_step",
@@ -104,6 +105,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.bz_quantize_fp8.argtypes = [vp, i32, i32, i32, f32, vp, vp, vp]
     lib.bz_dequant.restype = ctypes.c_int
     lib.bz_dequant.argtypes = [i32, vp, vp, vp, i32, i32, i32, vp, vp]
+    lib.bz_head_f32.restype = ctypes.c_int
+    lib.bz_head_f32.argtypes = [vp, i64, i32, i32, vp, i32, i64, i32, vp, i64, vp, i64, vp]
     lib.bz_qkv_rope_cache.restype = ctypes.c_int
     lib.bz_qkv_rope_cache.argtypes = [vp, i64, i32, i32, i32, i32, vp, vp, f32, vp, vp, i32, i64, vp, vp, vp, vp,
                                       i32, i32, vp, vp]

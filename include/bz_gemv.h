@@ -173,6 +173,22 @@ int bz_quantize_fp8(const void* w, int32_t w_dtype, int32_t N, int32_t K,
 int bz_dequant(int32_t wfmt, const void* w, const void* sc0, const void* sc1,
                int32_t N, int32_t K, int32_t group, void* out, void* stream);
 
+/* fp32 head GEMV: out[m][n] = sum_k x[m][k] * W[n][k], x, W and out fp32
+ * (fp32 products and sums).  W is one of nmat matrices [N][K] (K contiguous,
+ * 16-byte aligned rows) mat_stride floats apart, chosen on the device:
+ * sel = (index ? *index : 0) + index_offset, W = w + sel * mat_stride; a
+ * selection outside [0, nmat) writes zeros.  K % 4 == 0, K <= 4096.
+ * Replaces the fp32 head matmuls the reference keeps unquantized:
+ *   lm_head cast to fp32, input cast to fp32
+ *       models/cudagraph/backbone_graph.py:69-70,273
+ *   BreezeCodebooksHead.forward, codebook cache_position - 1
+ *       models/breeze.py:597-612, models/cudagraph/depth_decoder_graph.py:159-161
+ *       (its [hidden][vocab] weight is used here transposed to [vocab][hidden]) */
+int bz_head_f32(const float* x, int64_t ldx, int32_t M, int32_t K,
+                const float* w, int32_t N, int64_t mat_stride, int32_t nmat,
+                const int64_t* index, int64_t index_offset, float* out,
+                int64_t ldo, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

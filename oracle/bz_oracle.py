@@ -22,6 +22,8 @@ the reference's decode linears:
                            bench_gemv.py:31 (bf16-rounded x_hat)
 * ``gemv_ref``             models/fused/kernels.py:74-104 + 107-138 and the
                            dequantize-then-matmul definition bench_gemv.py:30-53
+* ``linear_f32_ref``       fp32 lm_head, models/cudagraph/backbone_graph.py:69-70,273
+* ``codebooks_head_ref``   BreezeCodebooksHead.forward, models/breeze.py:597-612
 * ``rel_err``              bench_gemv.py:53  max|out-ref| / max|ref|
 
 bfloat16 is handled as raw uint16 bit patterns (numpy has no bf16 dtype).
@@ -40,6 +42,8 @@ Pinning (what checks each function; see tests/test_oracle.py):
   gemv         - float64 brute-force loops on tiny shapes, linearity in x,
                  one-hot x selects one weight column, zero W gives 0 (+res)
   epilogues    - closed forms of SiLU(g)*u and +residual
+  fp32 heads   - torch's CPU float64 linear per codebook (a library routine);
+                 codebook selection by one-hot weights naming their codebook
 No function here is "parity unpinned": the reference publishes no golden
 vectors for this path (it has no automated test of it), so the pins above are
 the mathematics plus committed fixtures produced by this file.
@@ -356,6 +360,23 @@ def gemv_ref(xn, w_eff, epilogue: int = EPI_NONE, residual=None, row_scale=None)
     if epilogue == EPI_RES:
         return acc + np.asarray(residual, dtype=np.float64)
     return acc
+
+
+def linear_f32_ref(x, w) -> np.ndarray:
+    """The fp32 lm_head: float64 x @ W^T (models/cudagraph/backbone_graph.py:
+    69-70,273: weight and input cast to fp32)."""
+    return np.asarray(x, np.float64) @ np.asarray(w, np.float64).T
+
+
+def codebooks_head_ref(hidden, weight, cache_position=None) -> np.ndarray:
+    """BreezeCodebooksHead.forward (models/breeze.py:597-612): position i of
+    hidden [B, L, H] times weight[c] ([C, H, V]) with c = i when there is no
+    cache position and c = cache_position[i] - 1 otherwise."""
+    hidden = np.asarray(hidden, np.float64)
+    weight = np.asarray(weight, np.float64)
+    L = hidden.shape[1]
+    idx = np.arange(L) if cache_position is None else np.asarray(cache_position).reshape(-1) - 1
+    return np.stack([hidden[:, i, :] @ weight[idx[i]] for i in range(L)], axis=1)
 
 
 def rel_err(out, ref) -> float:

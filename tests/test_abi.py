@@ -275,3 +275,24 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(RuntimeError, match="no fallback"):
         _lib.lib()
+
+
+def test_head_f32_validation(L):
+    lib = L.lib()
+    f = 1 << 20
+    args = dict(x=f, ldx=1024, M=2, K=1024, w=f, N=2051, stride=2051 * 1024, nmat=15, index=None, off=0, out=f,
+                ldo=2051, stream=None)
+
+    def call(**kw):
+        a = dict(args)
+        a.update(kw)
+        return lib.bz_head_f32(*a.values())
+
+    assert call(x=None) == L.ERR_INVALID_ARG
+    assert call(M=0) == L.ERR_INVALID_ARG
+    assert call(nmat=0) == L.ERR_INVALID_ARG
+    assert call(K=1022, ldx=1024) == L.ERR_SHAPE          # K % 4
+    assert call(K=8192, ldx=8192) == L.ERR_SHAPE          # beyond the LDS staging of x
+    assert call(stride=100) == L.ERR_SHAPE                # matrices overlap
+    assert call(ldo=2000) == L.ERR_SHAPE
+    assert call(w=f + 4) == L.ERR_ALIGNMENT
