@@ -1,0 +1,113 @@
+"""Quantized checkpoint save / shells / load round trip and the int4 layout
+converter (CPU; the GPU forward round trip is in test_gpu_checkpoint.py).
+Mirrors the flow of the reference's test_quantized_checkpoint.py minus the
+model: describe -> save -> fresh skeleton -> install_shells -> load."""
+
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from oracle import bz_oracle as O
+
+from breeze_amd import quantized_checkpoint as Q
+from breeze_amd.fp8_linear import Fp8Linear
+from breeze_amd.int4_linear import LAYOUT, Int4Linear
+
+
+def _int4_shell(n, k, g, gen):
+    m = Int4Linear.__new__(Int4Linear)
+    nn.Module.__init__(m)
+    m.in_features, m.out_features, m.group_size = k, n, g
+    m.register_buffer("weight_int4", torch.randint(-2**31, 2**31 - 1, (n, k // 8), dtype=torch.int32, generator=gen))
+    m.register_buffer("scales_zeros", torch.randn(k // g, n, 2, generator=gen).to(torch.bfloat16))
+    return m
+
+
+def _fp8_shell(n, k, gen):
+    m = Fp8Linear.__new__(Fp8Linear)
+    nn.Module.__init__(m)
+    m.in_features, m.out_features = k, n
+    m.register_buffer("weight_fp8", torch.randn(n, k, generator=gen).to(torch.float8_e4m3fn))
+    m.register_buffer("weight_scale", torch.rand(1, n, generator=gen))
+    return m
+
+
+class _Block(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.norm = nn.LayerNorm(64)
+        self.mlp = nn.Module()
+        self.mlp.gate_proj = nn.Linear(64, 256, bias=False)
+        self.mlp.up_proj = nn.Linear(64, 256, bias=False)
+        self.mlp.down_proj = nn.Linear(256, 64, bias=False)
+
+
+def _quantized_block():
+    gen = torch.Generator().manual_seed(0)
+    blk = _Block()
+    blk.mlp.gate_proj = _int4_shell(256, 64, 32, gen)
+    blk.mlp.up_proj = _int4_shell(256, 64, 32, gen)
+    blk.mlp.down_proj = _fp8_shell(64, 256, gen)
+    return blk
+
+
+def test_round_trip(tmp_path):
+    blk = _quantized_block()
+    man = Q.save_quantized(blk, tmp_path, {"int4": "mlp"}, source="synthetic")
+    assert man["modules"]["mlp.gate_proj"]["layout"] == LAYOUT
+    assert man["modules"]["mlp.down_proj"]["kind"] == "fp8"
+    fresh = _Block()
+    manifest = Q.read_manifest(tmp_path)
+    assert Q.install_shells(fresh, manifest, "cpu") == 3
+    stats = Q.load_quantized_state(fresh, tmp_path, "cpu")
+    assert stats["missing"] == 0 and stats["unexpected"] == 0
+    for (ka, va), (kb, vb) in zip(sorted(blk.state_dict().items()), sorted(fresh.state_dict().items())):
+        assert ka == kb
+        assert torch.equal(va.view(torch.uint8) if va.dtype == torch.float8_e4m3fn else va,
+                           vb.view(torch.uint8) if vb.dtype == torch.float8_e4m3fn else vb), ka
+
+
+def test_shells_on_meta_and_host_prefixes(tmp_path):
+    Q.save_quantized(_quantized_block(), tmp_path, {}, source="synthetic")
+    fresh = _Block()
+    Q.install_shells(fresh, Q.read_manifest(tmp_path), "meta")
+    assert fresh.mlp.gate_proj.weight_int4.is_meta
+    stats = Q.load_quantized_state(fresh, tmp_path, "cpu", host_prefixes=("norm.",))
+    assert stats["missing"] == 0
+    assert not any(t.is_meta for t in list(fresh.parameters()) + list(fresh.buffers()))
+
+
+def test_refuses_foreign_layouts_kinds_and_versions(tmp_path):
+    Q.save_quantized(_quantized_block(), tmp_path, {}, source="synthetic")
+    man = Q.read_manifest(tmp_path)
+    no_tag = json.loads(json.dumps(man))
+    del no_tag["modules"]["mlp.gate_proj"]["layout"]
+    with pytest.raises(ValueError, match="tinygemm"):
+        Q.install_shells(_Block(), no_tag, "cpu")
+    int8 = json.loads(json.dumps(man))
+    int8["modules"]["mlp.up_proj"]["kind"] = "int8"
+    with pytest.raises(ValueError, match="not part of this build"):
+        Q.install_shells(_Block(), int8, "cpu")
+    man["version"] = 99
+    (tmp_path / Q.MANIFEST_NAME).write_text(json.dumps(man))
+    with pytest.raises(ValueError, match="unsupported checkpoint version"):
+        Q.read_manifest(tmp_path)
+
+
+def test_convert_logical_int4_matches_oracle_packing():
+    rng = np.random.default_rng(3)
+    q = rng.integers(0, 16, (48, 256), dtype=np.uint8)
+    odd_low = torch.from_numpy(O.pack_nibbles_odd_low(q))
+    sz = torch.randn(2, 48, 2).to(torch.bfloat16)
+    w4, sz2 = Q.convert_logical_int4(odd_low, sz, 128)
+    assert w4.dtype == torch.int32 and w4.shape == (48, 32)
+    np.testing.assert_array_equal(w4.view(torch.uint8).numpy(), O.pack_nibbles_even_low(q))
+    assert torch.equal(sz2, sz)
+    assert torch.equal(Q.logical_int4(w4), odd_low)
+    with pytest.raises(ValueError):
+        Q.convert_logical_int4(odd_low, torch.zeros(3, 48, 2), 128)
