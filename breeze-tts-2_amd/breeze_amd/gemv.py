@@ -20,6 +20,7 @@ from typing import Optional
 import torch
 
 from . import _lib
+from . import tuning as _tuning
 from ._lib import (
     DT_BF16,
     DT_F32,
@@ -92,6 +93,10 @@ def gemv(
 ) -> torch.Tensor:
     """out[M, N_out] = epilogue(rmsnorm?(x) @ w_eff^T) in one launch.
 
+    ``cfg`` (depth, waves, tiles, path) all zero takes the static per-arch
+    table's launch shape for this GEMV if it has one (tuning.py), else the
+    library's built-in rule.
+
     x [M, K] (any float dtype; computed as bf16), weight of format ``wfmt``
     with ``n`` rows, optional RMSNorm gamma [K], epilogue NONE / SILU_GATE
     (N_out = n/2) / RESIDUAL (residual [M, N_out]).  Returns ``out``.
@@ -138,7 +143,10 @@ def gemv(
     d.epilogue = epilogue
     d.out_dtype = _DT[out.dtype]
     d.residual_dtype = res_dt
-    d.cfg_depth, d.cfg_waves, d.cfg_tiles, d.cfg_path = (tuple(cfg) + (0, 0, 0, 0))[:4]
+    cfg = (tuple(cfg) + (0, 0, 0, 0))[:4]
+    if cfg == (0, 0, 0, 0):
+        cfg = _tuning.lookup(dev, n, K, wfmt, epilogue, gamma is not None, M) or cfg
+    d.cfg_depth, d.cfg_waves, d.cfg_tiles, d.cfg_path = cfg
     d.eps = eps
     d.x, d.ldx = x.data_ptr(), x.stride(0)
     d.w = w.data_ptr()

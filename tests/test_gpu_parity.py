@@ -308,3 +308,37 @@ def test_errors_raise():
         G.gemv(x, w, G.W_INT4_ZP, 8, sc0=sz, group=128)
     with pytest.raises(RuntimeError, match="invalid argument"):
         G.gemv(torch.zeros(1, 128, dtype=torch.bfloat16, device=_dev()), w, G.W_INT4_ZP, 8, group=128)
+
+
+@pytest.mark.parametrize("key", ["gfx950|1024|8192|2|2|0|1", "gfx950|2048|2048|0|2|0|2", "gfx950|4096|2048|3|0|1|1",
+                                 "gfx950|1536|1024|3|0|1|1"])
+def test_table_launch_shapes_match_oracle(key):
+    """Entries of the committed launch-shape table, run through gemv()'s
+    automatic selection, against the oracle."""
+    from breeze_amd import tuning
+
+    cfg = tuning.lookup(torch.device("cuda"), *[int(v) for v in key.split("|")[1:4]], int(key.split("|")[4]),
+                        key.split("|")[5] == "1", int(key.split("|")[6]))
+    assert cfg is not None, key
+    _, N, K, wfmt, epi, norm, M = (int(v) if i else v for i, v in enumerate(key.split("|")))
+    w, gamma, x = O.synth(N, K, M, seed=N + K)
+    n_out = N // 2 if epi == 1 else N
+    res_bits = O.f32_to_bf16_bits(np.random.default_rng(2).standard_normal((M, n_out)).astype(np.float32))
+    res = bf16_tensor(res_bits) if epi == 2 else None
+    g = bf16_tensor(gamma) if norm else None
+    if wfmt == G.W_INT4_ZP:
+        c = Int4Case(w, 128, symmetric=True)
+        out = G.gemv(bf16_tensor(x), c.d_packed, wfmt, N, sc0=c.d_sz, group=128, gamma=g, epilogue=epi, residual=res)
+        w_eff = c.w_zp
+    elif wfmt == G.W_FP8:
+        c = Fp8Case(w)
+        out = G.gemv(bf16_tensor(x), c.d_codes, wfmt, N, sc0=c.d_scale, gamma=g, epilogue=epi, residual=res)
+        w_eff = c.w_eff
+    else:
+        wb = O.f32_to_bf16_bits(w)
+        out = G.gemv(bf16_tensor(x), bf16_tensor(wb), wfmt, N, gamma=g, epilogue=epi, residual=res)
+        w_eff = O.bf16_bits_to_f32(wb)
+    xf = O.bf16_bits_to_f32(x)
+    xn = O.rmsnorm_f32(xf, O.bf16_bits_to_f32(gamma)) if norm else xf
+    ref = O.gemv_ref(xn, w_eff, epi, O.bf16_bits_to_f32(res_bits) if epi == 2 else None)
+    assert O.rel_err(f32(out), ref) <= TOL, key
