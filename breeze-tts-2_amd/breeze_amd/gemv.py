@@ -156,8 +156,42 @@ def gemv(
     if epilogue == EPI_RESIDUAL:
         d.residual, d.ldr = residual.data_ptr(), residual.stride(0)
     d.out, d.ldo = out.data_ptr(), out.stride(0)
+    if M >= _TILE_MIN_ROWS or cfg[3] == _PATH_TILE:
+        need = _lib.lib().bz_gemv_workspace(ctypes.byref(d))
+        if need:
+            ws = _workspace(dev, need)
+            d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel() * 4
     _lib.check(_lib.lib().bz_gemv(ctypes.byref(d), _lib.stream_of(x)), "bz_gemv")
     return out
+
+
+# The several-row tile kernel (path 4) runs from this many rows on; with more
+# than one K slice it needs a workspace (fp32 split-K partials and arrival
+# counters) that is zero-filled once and left zeroed by every call.
+_TILE_MIN_ROWS = 5
+_PATH_TILE = 4
+_GEMV_WS: dict = {}
+
+
+def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    """The device's GEMV workspace, grown (zero-filled) to at least nbytes.
+    One buffer per device, shared by every call on it: tile-path GEMVs on the
+    same device must not run concurrently on different streams (as with the
+    reference's cached split-K buffer, models/fused/kernels.py:179,192-198).  It
+    must be sized before a graph capture: an eager call of the same shape
+    (the graphs' warm-up steps) does that."""
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    buf = _GEMV_WS.get(key)
+    if buf is None or buf.numel() * 4 < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                f"GEMV workspace of {nbytes} bytes needed inside a graph capture; run the same call once "
+                "eagerly before capturing"
+            )
+        n = max(nbytes, 2 * (buf.numel() * 4 if buf is not None else 0), 1 << 20)
+        buf = torch.zeros(-(-n // 4), dtype=torch.int32, device=torch.device("cuda", key))
+        _GEMV_WS[key] = buf
+    return buf
 
 
 # ---- custom-op registration (torch.compile / fake tensors) -----------------

@@ -39,23 +39,25 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 // Two nibbles -> two bf16 values 128+q.  Selects nibble p = sel (low half)
 // and p = sel+4 (high half) of `v` after the caller's shift: the bf16 with
 // exponent 2^7 and the nibble as the low mantissa bits is exactly 128 + q.
-// One v_and_or_b32 (the mask comes from an SGPR, the exponent bits from a
-// VGPR: GFX9 VOP3 takes no literal and at most one SGPR).
-__device__ __forceinline__ uint32_t nib2_bf16(uint32_t v) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(0x000F000Fu), "v"(0x43004300u));
-    return r;
-}
+// Plain C++ that the compiler selects as one v_and_or_b32 (GFX9 VOP3 takes no
+// literal and at most one SGPR, so the mask sits in an SGPR and the exponent
+// bits in a VGPR).  It must stay visible to the compiler as a VALU
+// instruction: its result feeds v_mfma B operands, and the wait states a VALU
+// write needs before a matrix instruction reads the register are inserted by
+// the compiler's hazard pass, which does not see through inline assembly
+// (an inline-asm version gave wrong MFMA inputs when scheduled one
+// instruction ahead of the MFMA).
+__device__ __forceinline__ uint32_t nib2_bf16(uint32_t v) { return (v & 0x000F000Fu) | 0x43004300u; }
 
 // Same, with the mask and exponent bits supplied by the caller from
 // registers it keeps live (see NibbleConsts), so a hot loop does not
 // rematerialize them.
 __device__ __forceinline__ uint32_t nib2_bf16(uint32_t v, uint32_t mask_s, uint32_t magic_v) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(mask_s), "v"(magic_v));
-    return r;
+    return (v & mask_s) | magic_v;
 }
 
+// The two constants of nib2_bf16 in registers (an SGPR and a VGPR) whose
+// values the compiler cannot fold back into literals.
 struct NibbleConsts {
     uint32_t mask;   // SGPR: 0x000F000F
     uint32_t magic;  // VGPR: 0x43004300 (bf16 128.0 in both halves)

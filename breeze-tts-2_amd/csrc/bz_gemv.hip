@@ -1,12 +1,16 @@
 // Host dispatcher of the streaming decode GEMV (C ABI entry bz_gemv).  The
 // kernels are in bz_gemv_kernel.h (dot2 path), bz_gemv_mfma.h (bf16
-// matrix-core path) and bz_gemv_i8.h (int8 matrix-core path for int4
-// weights); their instances live in bz_gemv_{,mfma_,i8_}<fmt>.hip.
+// matrix-core path), bz_gemv_i8.h (int8 matrix-core path for int4 weights)
+// and bz_gemv_tile.h (several-row tile kernel); their instances live in
+// bz_gemv_{,mfma_,i8_,tile_}<fmt>.hip.
+#include <algorithm>
+
 #include "bz_gemv_i8.h"
+#include "bz_gemv_tile.h"
 
 namespace bz {
 
-enum { PATH_DOT2 = 1, PATH_MFMA = 2, PATH_I8 = 3 };
+enum { PATH_DOT2 = 1, PATH_MFMA = 2, PATH_I8 = 3, PATH_TILE = 4 };
 
 static int launch_wf(int wf, int path, const GemvParams& p, const Launch& l, hipStream_t st) {
     if (path == PATH_I8) {
@@ -34,16 +38,15 @@ constexpr int kMaxRowsPerLaunch = 4;
 // MI355X (256 CUs), each owning tiles / 256 consecutive output tiles.
 constexpr int kTargetWorkgroups = 256;
 
-}  // namespace bz
+// Descriptor checks shared by bz_gemv and bz_gemv_workspace; fills the
+// derived sizes.
+struct DescInfo {
+    int n_out, glog2;
+    int64_t row_bytes;
+    bool i4;
+};
 
-using namespace bz;
-
-extern "C" size_t bz_gemv_workspace(const bz_gemv_desc* d) {
-    (void)d;
-    return 0;
-}
-
-extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
+static int check_desc(const bz_gemv_desc* d, DescInfo& di) {
     if (!d) return BZ_ERR_INVALID_ARG;
     if (d->abi_version != BZ_ABI_VERSION) return BZ_ERR_ABI;
     const int M = d->M, N = d->N, K = d->K, wf = d->wfmt, epi = d->epilogue;
@@ -86,6 +89,166 @@ extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
         if (!aligned(d->sc0, 2) || !aligned(d->sc1, 2)) return BZ_ERR_ALIGNMENT;
     }
     if (!aligned(d->out, d->out_dtype == BZ_DT_F32 ? 4 : 2)) return BZ_ERR_ALIGNMENT;
+    if (d->cfg_path < 0 || d->cfg_path > PATH_TILE) return BZ_ERR_INVALID_ARG;
+    di.n_out = n_out;
+    di.glog2 = glog2;
+    di.row_bytes = row_bytes;
+    di.i4 = i4;
+    return BZ_OK;
+}
+
+// Launch shape of the several-row tile kernel (bz_gemv_tile.h).
+struct TilePlan {
+    int MB, T, D, ks, nsl, ncb;
+    size_t lds, ws;
+};
+
+// x slice bytes the automatic rule allows per workgroup (two workgroups per
+// CU fit the 160 KB of LDS), and the workgroups it aims for (two per CU).
+constexpr int kTileXBudget = 64 * 1024;
+constexpr int kTileTargetWorkgroups = 512;
+
+// BZ_OK and the plan of one launch over M <= kTileMaxRows rows when the tile
+// kernel can run this descriptor (its cfg_* fields are read when cfg_path
+// selects it); otherwise an error code.  Fewer rows never need more slices,
+// LDS or workspace than more rows.
+static int tile_plan(const bz_gemv_desc* d, const DescInfo& di, int M, TilePlan& pl) {
+    const int K = d->K, wf = d->wfmt;
+    const bool forced = d->cfg_path == PATH_TILE;
+    if (d->gamma || d->epilogue == BZ_EPI_SILU_GATE) return BZ_ERR_UNSUPPORTED;
+    const int UK = mfma_unit_k(wf);
+    if ((di.i4 && d->group < 128) || K % UK || di.row_bytes >= (1 << 24)) return BZ_ERR_UNSUPPORTED;
+    pl.MB = (M + 15) / 16;
+    pl.T = forced && d->cfg_tiles ? d->cfg_tiles : 1;
+    pl.D = forced && d->cfg_depth ? d->cfg_depth : 4;
+    if ((pl.T != 1 && pl.T != 2) || (pl.D != 2 && pl.D != 4 && pl.D != 8)) return BZ_ERR_INVALID_ARG;
+    const int cbw = kTileWaves * 16 * pl.T;
+    pl.ncb = (di.n_out + cbw - 1) / cbw;
+    if (pl.ncb > kTileCounters) return BZ_ERR_UNSUPPORTED;
+    const int units = K / UK;
+    int nsl;
+    if (forced && d->cfg_waves) {
+        nsl = d->cfg_waves;
+    } else {
+        const int want = (kTileTargetWorkgroups + pl.ncb - 1) / pl.ncb;
+        const int max_units = std::max(1, (kTileXBudget / (2 * M) - 8) / UK);
+        const int need = (units + max_units - 1) / max_units;
+        nsl = std::max(want, need);
+    }
+    if (nsl < 1) return BZ_ERR_INVALID_ARG;
+    nsl = std::min(nsl, units);
+    const int upl = (units + nsl - 1) / nsl;  // units per slice
+    pl.ks = upl * UK;
+    pl.nsl = (units + upl - 1) / upl;
+    pl.lds = (size_t)tile_lds_layout(M, pl.MB, pl.ks, wf).total;
+    if (pl.lds > (size_t)device_lds_limit()) return BZ_ERR_UNSUPPORTED;
+    pl.ws = pl.nsl > 1 ? kTilePartOffset + (size_t)pl.nsl * M * di.n_out * 4 : 0;
+    return BZ_OK;
+}
+
+// The automatic rule takes the tile kernel from this many rows on.
+constexpr int kTileMinRows = 5;
+
+static bool tile_auto(const bz_gemv_desc* d) { return d->cfg_path == 0 && d->M >= kTileMinRows; }
+
+static int launch_tile(int wf, const TileParams& tp, const TileLaunch& l, hipStream_t st) {
+    switch (wf) {
+        case WF_I4ZP: return launch_tile_i4zp(tp, l, st);
+        case WF_I4MIN: return launch_tile_i4min(tp, l, st);
+        case WF_FP8: return launch_tile_fp8(tp, l, st);
+        case WF_BF16: return launch_tile_bf16(tp, l, st);
+        default: return BZ_ERR_INVALID_ARG;
+    }
+}
+
+}  // namespace bz
+
+using namespace bz;
+
+extern "C" size_t bz_gemv_workspace(const bz_gemv_desc* d) {
+    DescInfo di;
+    if (check_desc(d, di) != BZ_OK) return 0;
+    if (d->cfg_path != PATH_TILE && !tile_auto(d)) return 0;
+    TilePlan pl{};
+    return tile_plan(d, di, std::min(d->M, kTileMaxRows), pl) == BZ_OK ? pl.ws : 0;
+}
+
+extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
+    DescInfo di;
+    const int rc0 = check_desc(d, di);
+    if (rc0 != BZ_OK) return rc0;
+    const int M = d->M, N = d->N, K = d->K, wf = d->wfmt, epi = d->epilogue;
+    const int n_out = di.n_out, glog2 = di.glog2;
+    const int64_t row_bytes = di.row_bytes;
+    const bool i4 = di.i4;
+
+    // several-row tile kernel (forced, or automatic from kTileMinRows rows on
+    // when the caller passed the workspace it needs): kTileMaxRows rows per
+    // launch
+    if (d->cfg_path == PATH_TILE || tile_auto(d)) {
+        TilePlan pl{};
+        const int trc = tile_plan(d, di, std::min(M, kTileMaxRows), pl);
+        bool ws_ok = pl.ws == 0;
+        if (trc == BZ_OK && pl.ws)
+            ws_ok = d->workspace && aligned(d->workspace, 16) && d->workspace_bytes >= pl.ws;
+        if (d->cfg_path == PATH_TILE) {
+            if (trc != BZ_OK) return trc;
+            if (!ws_ok) return BZ_ERR_INVALID_ARG;
+        }
+        if (trc == BZ_OK && ws_ok) {
+            TileParams tp;
+            GemvParams& p = tp.p;
+            p.w = static_cast<const uint8_t*>(d->w);
+            p.row_bytes = row_bytes;
+            p.sc0 = d->sc0;
+            p.sc1 = d->sc1;
+            p.gamma = nullptr;
+            p.ldx = d->ldx;
+            p.ldr = d->ldr;
+            p.ldo = d->ldo;
+            p.eps = d->eps;
+            p.N = N;
+            p.K = K;
+            p.G = i4 ? K / d->group : 0;
+            p.glog2 = glog2;
+            p.n_out = n_out;
+            p.nchunks = 0;
+            p.ntiles = 0;
+            p.tpw = 0;
+            p.epi = epi;
+            p.out_f32 = d->out_dtype == BZ_DT_F32;
+            p.res_f32 = d->residual_dtype == BZ_DT_F32;
+            p.norm = 0;
+            tp.cnt = static_cast<uint32_t*>(d->workspace);
+            // the plan of a last, shorter launch (checked before anything is launched)
+            TilePlan pl_rem = pl;
+            if (M > kTileMaxRows && M % kTileMaxRows && tile_plan(d, di, M % kTileMaxRows, pl_rem) != BZ_OK)
+                return BZ_ERR_UNSUPPORTED;
+            const size_t osz = p.out_f32 ? 4 : 2, rsz = p.res_f32 ? 4 : 2;
+            hipStream_t st = static_cast<hipStream_t>(stream);
+            for (int m0 = 0; m0 < M; m0 += kTileMaxRows) {
+                const int rows = std::min(M - m0, kTileMaxRows);
+                const TilePlan& q = rows == std::min(M, kTileMaxRows) ? pl : pl_rem;
+                p.x = static_cast<const uint16_t*>(d->x) + (int64_t)m0 * d->ldx;
+                p.out = static_cast<uint8_t*>(d->out) + (int64_t)m0 * d->ldo * osz;
+                p.res = d->residual ? static_cast<const uint8_t*>(d->residual) + (int64_t)m0 * d->ldr * rsz : nullptr;
+                tp.M = rows;
+                tp.ks = q.ks;
+                tp.nsl = q.nsl;
+                tp.part = q.ws ? reinterpret_cast<float*>(static_cast<uint8_t*>(d->workspace) + kTilePartOffset)
+                               : nullptr;
+                TileLaunch l;
+                l.MB = q.MB;
+                l.T = q.T;
+                l.D = q.D;
+                l.lds = q.lds;
+                l.grid = (unsigned)(q.ncb * q.nsl);
+                const int rc = launch_tile(wf, tp, l, st);
+                if (rc != BZ_OK) return rc;
+            }
+            return BZ_OK;
+        }
+    }
 
     const bool silu = epi == BZ_EPI_SILU_GATE;
     const int T = silu ? 2 : 1;
@@ -93,7 +256,6 @@ extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
     // group (group >= 128); the int8 one also whole units (K % 128 == 0).
     const bool mfma_ok = !i4 || d->group >= 128;
     const bool i8_ok = i4 && d->group >= 128 && K % 128 == 0;
-    if (d->cfg_path < 0 || d->cfg_path > 3) return BZ_ERR_INVALID_ARG;
     if ((d->cfg_path == 2 && !mfma_ok) || (d->cfg_path == 3 && !i8_ok)) return BZ_ERR_UNSUPPORTED;
     // Automatic choice (measured on MI355X, M = 1..16): the int8 matrix-core
     // path for several rows over short rows (K <= 4096: every workgroup

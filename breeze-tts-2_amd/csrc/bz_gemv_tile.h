@@ -1,0 +1,390 @@
+// Several-row tile kernel of the decode GEMV (gfx950 MFMA): M = 1..32 rows
+// of x against int4 / fp8 / bf16 weights, every weight byte streamed from HBM
+// once per launch.
+//
+// The row-sliced streaming kernels (bz_gemv_mfma.h, bz_gemv_i8.h) hold at
+// most 4 rows of x per launch (16 on the int8 path for rows of <= 4096 k), so
+// 16 or 32 rows re-stream the weights 2-8 times.  Here a workgroup owns a
+// column block (4 waves x T tiles of 16 output columns) and one K slice:
+//   * grid = column blocks x K slices; block b takes column block b / nsl and
+//     slice b % nsl, so the slices of one column block run back to back and
+//     its last arrival finds the partials recently written;
+//   * the slice of x for all M rows (bf16) is staged in LDS, rows padded by
+//     16 bytes so the 16 rows read by one quarter-wave hit distinct banks; the
+//     first loads of x are issued before the first weights, so waiting for x
+//     does not wait behind the weights (vector loads retire in order);
+//   * a wave streams its T tiles over the slice's 64-byte units with the
+//     operand placement of the bf16 MFMA kernel: lane l loads 16 bytes of
+//     weight row l%16 at offset 16*(l/16) (the B operand of
+//     v_mfma_f32_16x16x32_bf16), and MB = 1 or 2 A operands of 16 x rows
+//     (rows 0-15, 16-31) come from LDS, so each unpacked weight feeds 16 or
+//     32 rows;
+//   * int4 units are scaled per group as in the bf16 MFMA kernel,
+//     y += s * D + (z - 136 s) * X with X the unit's sum of x per row, kept
+//     in LDS as [unit][row] so the 4 rows of a lane come in one 16-byte read;
+//   * one slice: the epilogue (fp8 row scale, residual) is applied straight
+//     from the accumulators.  Several slices: fp32 partials go to the
+//     workspace with agent-scope stores (they reach the point of coherence
+//     without an L2 write-back), each workgroup waits for its stores, counts
+//     its arrival on the column block's counter, and the last one sums the
+//     slices in slice order (the result does not depend on arrival order),
+//     applies the epilogue and resets the counter to zero for the next call.
+//
+// Workspace: kTileCounters uint32 counters (zero before the first call; every
+// call leaves them zero), then fp32 partials [nsl][M][N_out].
+#pragma once
+#include "bz_gemv_mfma.h"
+
+namespace bz {
+
+constexpr int kTileThreads = 256;
+constexpr int kTileWaves = kTileThreads / 64;
+constexpr int kTileXB = 8;            // 16-byte blocks of x per thread loaded ahead of the weights
+constexpr int kTileCounters = 4096;   // column blocks per launch (counters at the workspace start)
+constexpr size_t kTilePartOffset = (size_t)kTileCounters * 4;
+constexpr int kTileMaxRows = 32;
+
+struct TileParams {
+    GemvParams p;
+    int M;      // rows of x (<= 16 * MB)
+    int ks;     // k per slice (a multiple of the format's unit)
+    int nsl;    // K slices
+    uint32_t* cnt;
+    float* part;
+};
+
+struct TileLaunch {
+    int MB, T, D;
+    size_t lds;
+    unsigned grid;
+};
+
+// LDS row of x in elements: the slice plus 16 bytes of padding.
+__host__ __device__ inline int tile_xrow(int ks) { return ks + 8; }
+
+// LDS: x rows, the int4 unit sums, the last-arrival flag.  All of it is
+// dynamic (no static __shared__), so a launch may raise the dynamic limit to
+// the whole LDS.
+struct TileLds {
+    int xs, x128, flag, total;
+};
+__host__ __device__ inline TileLds tile_lds_layout(int M, int MB, int ks, int wf) {
+    TileLds L;
+    L.xs = 0;
+    L.x128 = align16(M * tile_xrow(ks) * 2);
+    L.flag = L.x128 + (is_int4(wf) ? align16((ks / 128) * 16 * MB * 4) : 0);
+    L.total = L.flag + 16;
+    return L;
+}
+
+// Stage one 8-element block of x row m at slice element 8*kq.  int4 blocks
+// are permuted [x0 x4 x1 x5 x2 x6 x3 x7] to pair with the nibble pairs, and
+// 16 consecutive lanes (one 128-k unit of one row) sum their blocks into
+// x128[unit][row].
+template <int WF>
+__device__ __forceinline__ void tile_stage(u32x4 v, int m, int kq, uint16_t* xs, float* x128, int xrow, int rstride) {
+    u32x4 o = v;
+    if (is_int4(WF)) {
+        o[0] = (v[0] & 0xFFFFu) | (v[2] << 16);
+        o[1] = (v[0] >> 16) | (v[2] & 0xFFFF0000u);
+        o[2] = (v[1] & 0xFFFFu) | (v[3] << 16);
+        o[3] = (v[1] >> 16) | (v[3] & 0xFFFF0000u);
+        float cs = ((bf16_lo(v[0]) + bf16_hi(v[0])) + (bf16_lo(v[1]) + bf16_hi(v[1]))) +
+                   ((bf16_lo(v[2]) + bf16_hi(v[2])) + (bf16_lo(v[3]) + bf16_hi(v[3])));
+        cs = sum16(cs);
+        if ((kq & 15) == 0) x128[(kq >> 4) * rstride + m] = cs;
+    }
+    *reinterpret_cast<u32x4*>(xs + m * xrow + kq * 8) = o;
+}
+
+// Epilogue of one output: fp8 row scale, residual, store.
+template <int WF>
+__device__ __forceinline__ void tile_store(const GemvParams& p, float v, int r, int c) {
+    if (WF == WF_FP8) v *= reinterpret_cast<const float*>(p.sc0)[c];
+    if (p.epi == BZ_EPI_RESIDUAL) {
+        const int64_t idx = (int64_t)r * p.ldr + c;
+        v += p.res_f32 ? reinterpret_cast<const float*>(p.res)[idx]
+                       : bf16_to_f32(reinterpret_cast<const uint16_t*>(p.res)[idx]);
+    }
+    const int64_t oi = (int64_t)r * p.ldo + c;
+    if (p.out_f32)
+        reinterpret_cast<float*>(p.out)[oi] = v;
+    else
+        reinterpret_cast<uint16_t*>(p.out)[oi] = f32_to_bf16(v);
+}
+
+template <int WF, int MB, int T, int D>
+__global__ void __launch_bounds__(kTileThreads) gemv_tile(TileParams tp) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const GemvParams& p = tp.p;
+    constexpr int UK = mfma_unit_k(WF);
+    constexpr int RS = 16 * MB;  // x128 row stride (rows per unit)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 15, kb = lane >> 4;
+    const int M = tp.M, nsl = tp.nsl;
+    const int cb = (int)blockIdx.x / nsl, sl = (int)blockIdx.x - cb * nsl;
+    const int k0 = sl * tp.ks;
+    const int kl = min(tp.ks, p.K - k0);  // host: a multiple of UK, > 0
+    const int nu = kl / UK;
+    const int xrow = tile_xrow(tp.ks);
+    const int col0 = (cb * kTileWaves + wave) * 16 * T;  // wave-uniform
+    const bool active = col0 < p.n_out;
+
+    const TileLds L = tile_lds_layout(M, MB, tp.ks, WF);
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem + L.xs);
+    float* x128 = reinterpret_cast<float*>(smem + L.x128);
+    int& last_arrival = *reinterpret_cast<int*>(smem + L.flag);
+
+    // 0. the first blocks of the x slice (indices clamped: straight-line loads)
+    const int nblk = kl >> 3, total = M * nblk;
+    u32x4 xr[kTileXB];
+#pragma unroll
+    for (int i = 0; i < kTileXB; ++i) {
+        const int bi = min(tid + i * kTileThreads, total - 1);
+        const int m = bi / nblk;
+        xr[i] = ldg16(p.x + (int64_t)m * p.ldx + k0 + (bi - m * nblk) * 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 1. the first D units of weights (+ int4 group scales)
+    u32x4 buf[D][T];
+    uint32_t scb[D][T];
+    const int ub0 = k0 / UK;
+    uint32_t loff[T];  // lane offset inside the tile: row (clamped to the last column) and 16-byte slot
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const int lr = min(j, max(p.n_out - 1 - (col0 + 16 * t), 0));
+        loff[t] = __umul24((uint32_t)lr, (uint32_t)p.row_bytes) + (uint32_t)(kb * 16);
+    }
+    auto issue = [&](int d, StepCursor c) {
+        const int u = ub0 + c.ch;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int ct = min(col0 + 16 * t, p.n_out - 1);
+            const uint8_t* base = p.w + (int64_t)ct * p.row_bytes + (int64_t)u * 64;  // uniform
+            buf[d][t] = ldg16(base + loff[t]);
+            if (is_int4(WF)) {
+                const int row = min(col0 + 16 * t + j, p.n_out - 1);
+                const int g = (u * 128) >> p.glog2;
+                if (WF == WF_I4ZP)
+                    scb[d][t] = reinterpret_cast<const uint32_t*>(p.sc0)[(int64_t)g * p.N + row];
+                else
+                    scb[d][t] = (uint32_t)reinterpret_cast<const uint16_t*>(p.sc0)[(int64_t)row * p.G + g] |
+                                ((uint32_t)reinterpret_cast<const uint16_t*>(p.sc1)[(int64_t)row * p.G + g] << 16);
+            }
+        }
+    };
+    StepCursor ic{0, 0};
+    if (active) pipeline_prime<0, D>(nu, 1, nu, 0, ic, issue);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. stage x (the rest of the slice is loaded here, behind the weights)
+#pragma unroll
+    for (int i = 0; i < kTileXB; ++i) {
+        const int bi = tid + i * kTileThreads;
+        if (bi < total) {  // uniform over each 16-lane group (total % 16 == 0 for int4)
+            const int m = bi / nblk;
+            tile_stage<WF>(xr[i], m, bi - m * nblk, xs, x128, xrow, RS);
+        }
+    }
+    for (int bi = tid + kTileXB * kTileThreads; bi < total; bi += kTileThreads) {
+        const int m = bi / nblk, kq = bi - m * nblk;
+        tile_stage<WF>(ldg16(p.x + (int64_t)m * p.ldx + k0 + kq * 8), m, kq, xs, x128, xrow, RS);
+    }
+    __syncthreads();
+
+    // 3. every unit of the slice
+    f32x4_t acc[T][MB];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[t][mb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const uint16_t* xa[MB];  // this lane's A row (clamped to the last row of x) at its 16-byte slot
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+        xa[mb] = xs + min(16 * mb + j, M - 1) * xrow + kb * (is_int4(WF) ? 32 : (WF == WF_FP8 ? 16 : 8));
+    const NibbleConsts nc;
+    auto consume = [&](int d, StepCursor c) {
+        const int u = c.ch;
+        if (is_int4(WF)) {
+            u32x4 a[MB][4];
+            f32x4_t X[MB];
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+                for (int dd = 0; dd < 4; ++dd) a[mb][dd] = *reinterpret_cast<const u32x4*>(xa[mb] + u * 128 + dd * 8);
+                X[mb] = *reinterpret_cast<const f32x4_t*>(x128 + u * RS + 16 * mb + 4 * kb);
+            }
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                f32x4_t dacc[MB];
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) dacc[mb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int dd = 0; dd < 4; ++dd) {
+                    u32x4 bv;
+#pragma unroll
+                    for (int sh = 0; sh < 4; ++sh) bv[sh] = nib2_bf16(buf[d][t][dd] >> (4 * sh), nc.mask, nc.magic);
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb) dacc[mb] = mfma_bf16(a[mb][dd], bv, dacc[mb]);
+                }
+                const uint32_t e = scb[d][t];
+                const float s = bf16_lo(e);
+                const float zp = bf16_hi(e) - (WF == WF_I4ZP ? 136.0f : 128.0f) * s;
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[t][mb][q] += s * dacc[mb][q] + zp * X[mb][q];
+            }
+        } else if (WF == WF_FP8) {
+            u32x4 a0[MB], a1[MB];
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                a0[mb] = *reinterpret_cast<const u32x4*>(xa[mb] + u * 64);
+                a1[mb] = *reinterpret_cast<const u32x4*>(xa[mb] + u * 64 + 8);
+            }
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const u32x4 w = buf[d][t];
+                const u32x4 b0 = {fp8x2_bf16<false>(w[0]), fp8x2_bf16<true>(w[0]), fp8x2_bf16<false>(w[1]),
+                                  fp8x2_bf16<true>(w[1])};
+                const u32x4 b1 = {fp8x2_bf16<false>(w[2]), fp8x2_bf16<true>(w[2]), fp8x2_bf16<false>(w[3]),
+                                  fp8x2_bf16<true>(w[3])};
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    acc[t][mb] = mfma_bf16(a0[mb], b0, acc[t][mb]);
+                    acc[t][mb] = mfma_bf16(a1[mb], b1, acc[t][mb]);
+                }
+            }
+        } else {
+            u32x4 a0[MB];
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) a0[mb] = *reinterpret_cast<const u32x4*>(xa[mb] + u * 32);
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) acc[t][mb] = mfma_bf16(a0[mb], buf[d][t], acc[t][mb]);
+        }
+    };
+    if (active) pipeline_run<D>(nu, 1, nu, 0, ic, issue, consume);
+
+    // 4a. one slice: epilogue from the accumulators (lane: column j of each
+    //     tile, rows 16 mb + 4 kb + q)
+    if (nsl == 1) {
+        if (!active) return;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int c = col0 + 16 * t + j;
+            if (c >= p.n_out) continue;
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int r = 16 * mb + 4 * kb + q;
+                    if (r < M) tile_store<WF>(p, acc[t][mb][q], r, c);
+                }
+        }
+        return;
+    }
+
+    // 4b. several slices: partials, arrival, and the last arrival's sum
+    if (active) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int c = col0 + 16 * t + j;
+            if (c >= p.n_out) continue;
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int r = 16 * mb + 4 * kb + q;
+                    if (r < M)
+                        __hip_atomic_store(tp.part + ((int64_t)sl * M + r) * p.n_out + c, acc[t][mb][q],
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(&tp.cnt[cb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_arrival = prev == (unsigned)nsl - 1u;
+    }
+    __syncthreads();
+    if (!last_arrival) return;
+    constexpr int CBW = kTileWaves * 16 * T;  // columns of a block
+    const int nout = M * CBW;
+    for (int i0 = 0; i0 < nout; i0 += 4 * kTileThreads) {
+        float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s0 = 0; s0 < nsl; s0 += 8) {
+            float v[4][8];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int i = min(i0 + tid + q * kTileThreads, nout - 1);
+                const int r = i / CBW;
+                const int c = min(cb * CBW + (i - r * CBW), p.n_out - 1);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int s = min(s0 + u, nsl - 1);
+                    v[q][u] = __hip_atomic_load(tp.part + ((int64_t)s * M + r) * p.n_out + c, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (s0 + u < nsl) sum[q] += v[q][u];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int i = i0 + tid + q * kTileThreads;
+            if (i >= nout) continue;
+            const int r = i / CBW;
+            const int c = cb * CBW + (i - r * CBW);
+            if (c < p.n_out) tile_store<WF>(p, sum[q], r, c);
+        }
+    }
+    if (tid == 0) __hip_atomic_store(&tp.cnt[cb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int WF, int MB, int T, int D>
+int launch_tile_kernel(const TileParams& tp, const TileLaunch& l, hipStream_t st) {
+    auto kern = gemv_tile<WF, MB, T, D>;
+    if (l.lds > 65536) {
+        static std::atomic<bool> raised{false};
+        if (!raised.load(std::memory_order_relaxed)) {
+            if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    device_lds_limit()) != hipSuccess)
+                return BZ_ERR_LAUNCH;
+            raised.store(true, std::memory_order_relaxed);
+        }
+    }
+    hipLaunchKernelGGL(kern, dim3(l.grid), dim3(kTileThreads), l.lds, st, tp);
+    return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
+}
+
+template <int WF, int MB, int T>
+int launch_tile_depth(const TileParams& tp, const TileLaunch& l, hipStream_t st) {
+    switch (l.D) {
+        case 2: return launch_tile_kernel<WF, MB, T, 2>(tp, l, st);
+        case 4: return launch_tile_kernel<WF, MB, T, 4>(tp, l, st);
+        case 8: return launch_tile_kernel<WF, MB, T, 8>(tp, l, st);
+        default: return BZ_ERR_INVALID_ARG;
+    }
+}
+
+template <int WF>
+int launch_tile_wf(const TileParams& tp, const TileLaunch& l, hipStream_t st) {
+    if (l.MB == 1) return l.T == 1 ? launch_tile_depth<WF, 1, 1>(tp, l, st) : launch_tile_depth<WF, 1, 2>(tp, l, st);
+    if (l.MB == 2) return l.T == 1 ? launch_tile_depth<WF, 2, 1>(tp, l, st) : launch_tile_depth<WF, 2, 2>(tp, l, st);
+    return BZ_ERR_INVALID_ARG;
+}
+
+int launch_tile_i4zp(const TileParams& tp, const TileLaunch& l, hipStream_t st);
+int launch_tile_i4min(const TileParams& tp, const TileLaunch& l, hipStream_t st);
+int launch_tile_fp8(const TileParams& tp, const TileLaunch& l, hipStream_t st);
+int launch_tile_bf16(const TileParams& tp, const TileLaunch& l, hipStream_t st);
+
+}  // namespace bz

@@ -90,8 +90,23 @@ typedef enum bz_dtype {
  * and arithmetic path (1 = v_dot2 kernel, 8-column tiles; 2 = bf16 MFMA
  * kernel, 16-column tiles, needs an int4 group >= 128; 3 = int8 MFMA kernel
  * for int4 weights, group >= 128 and K % 128 == 0, x held as two int8
- * planes per row (about 16 significant bits), up to 16 rows per launch).
+ * planes per row (about 16 significant bits), up to 16 rows per launch;
+ * 4 = several-row bf16 MFMA tile kernel, see below).
  * Used by tuning sweeps.
+ *
+ * Several rows (path 4).  Up to 32 rows of x per launch stream every weight
+ * byte once: a workgroup owns 64 * cfg_tiles output columns (cfg_tiles 1 or
+ * 2) and one K slice, and cfg_waves (path 4 only) sets the number of K
+ * slices (0: about 512 workgroups, x slice <= 64 KB of LDS).  It needs no
+ * RMSNorm (gamma NULL), epilogue NONE or RESIDUAL, an int4 group >= 128 and
+ * K a multiple of 128 (int4), 64 (fp8) or 32 (bf16); larger M runs 32 rows
+ * per launch.  With more than one K slice the slices' fp32 partials go to
+ * `workspace` (bz_gemv_workspace bytes, 16-byte aligned, zero-filled before
+ * its first use; every call leaves its counters zero again, so it is never
+ * cleared afterwards and calls can be recorded into a graph).  Calls that
+ * share a workspace must not run concurrently.  The automatic rule takes
+ * this path from M = 5 on when `workspace` is large enough (or none is
+ * needed), else it keeps the row-sliced paths.
  */
 typedef struct bz_gemv_desc {
     int32_t abi_version;      /* must be BZ_ABI_VERSION */
@@ -110,7 +125,7 @@ typedef struct bz_gemv_desc {
     const void* gamma;
     const void* residual; int64_t ldr;
     void* out; int64_t ldo;
-    void* workspace; size_t workspace_bytes;  /* reserved: current kernels need none */
+    void* workspace; size_t workspace_bytes;  /* path 4 split-K partials + counters */
 } bz_gemv_desc;
 
 /* ABI version of the loaded library (BZ_ABI_VERSION it was built with). */
@@ -119,8 +134,10 @@ int bz_abi_version(void);
 /* Static description of a status code. */
 const char* bz_strerror(int status);
 
-/* Workspace bytes bz_gemv needs for this descriptor (0 for every shape the
- * current kernels run: partial sums never leave the workgroup). */
+/* Workspace bytes the several-row tile path (path 4) needs for this
+ * descriptor: 0 when bz_gemv would not take that path (M < 5 without
+ * cfg_path 4, an RMSNorm or SiLU-gate call, unsupported K or group) or runs
+ * it with a single K slice.  Returns 0 for an invalid descriptor. */
 size_t bz_gemv_workspace(const bz_gemv_desc* d);
 
 /* The fused decode GEMV.  Replaces, as one launch:

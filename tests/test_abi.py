@@ -146,9 +146,41 @@ def test_gemv_null_descriptor(L):
     assert L.lib().bz_gemv(None, None) == L.ERR_INVALID_ARG
 
 
-def test_workspace_is_zero(L):
-    d = _desc(L)
-    assert L.lib().bz_gemv_workspace(ctypes.byref(d)) == 0
+def test_workspace_sizes(L):
+    """0 below 5 rows, with an RMSNorm or a SiLU gate, or for an invalid
+    descriptor; otherwise the counters (16 KB) plus nsl x M x N fp32
+    partials of the several-row tile path."""
+    ws = lambda **kw: L.lib().bz_gemv_workspace(ctypes.byref(_desc(L, **kw)))  # noqa: E731
+    assert ws() == 0
+    assert ws(M=4) == 0
+    # N = 64: one column block, so the rule asks for the most slices: K / 128 = 2
+    assert ws(M=8) == 16384 + 2 * 8 * 64 * 4
+    assert ws(M=32, K=1024, ldx=1024) == 16384 + 8 * 32 * 64 * 4
+    assert ws(M=40, K=1024, ldx=1024) == 16384 + 8 * 32 * 64 * 4  # 32 rows per launch
+    assert ws(M=8, gamma=1 << 20) == 0
+    assert ws(M=8, N=128, epilogue=1) == 0
+    assert ws(M=8, abi_version=99) == 0
+    assert ws(M=2, cfg_path=4, cfg_waves=1) == 0               # one slice: no partials
+    assert ws(M=2, cfg_path=4, cfg_waves=2) == 16384 + 2 * 2 * 64 * 4
+
+
+@pytest.mark.parametrize(
+    "kw,status",
+    [
+        ({"cfg_path": 5}, "ERR_INVALID_ARG"),
+        ({"cfg_path": 4, "M": 8}, "ERR_INVALID_ARG"),                       # split-K needs the workspace
+        ({"cfg_path": 4, "M": 8, "workspace": 1 << 20, "workspace_bytes": 100}, "ERR_INVALID_ARG"),
+        ({"cfg_path": 4, "M": 8, "cfg_tiles": 3}, "ERR_INVALID_ARG"),
+        ({"cfg_path": 4, "M": 8, "cfg_depth": 16}, "ERR_INVALID_ARG"),
+        ({"cfg_path": 4, "M": 8, "gamma": 1 << 20}, "ERR_UNSUPPORTED"),     # no RMSNorm prologue
+        ({"cfg_path": 4, "M": 8, "N": 128, "epilogue": 1}, "ERR_UNSUPPORTED"),  # no SiLU gate
+        ({"cfg_path": 4, "M": 8, "group": 64}, "ERR_UNSUPPORTED"),          # int4 group >= 128
+        ({"cfg_path": 4, "M": 8, "wfmt": 2, "K": 272, "ldx": 272}, "ERR_UNSUPPORTED"),  # fp8 K % 64
+    ],
+)
+def test_tile_path_validation(L, kw, status):
+    d = _desc(L, **kw)
+    assert L.lib().bz_gemv(ctypes.byref(d), None) == getattr(L, status)
 
 
 def test_aux_validation(L):
