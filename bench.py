@@ -29,6 +29,12 @@ same counter reads for a plain 256 MiB elementwise copy):
   rocprofv3 --pmc FETCH_SIZE --output-format csv -d D1 -o run -- python3 bench.py --profile-gateup
   rocprofv3 --pmc WRITE_SIZE --output-format csv -d D2 -o run -- python3 bench.py --profile-gateup
   python3 bench.py --pmc-summary D1 D2      (prints the traffic summary)
+
+Matrix-core use of the several-row tile GEMVs (C4 shapes at M = 16 and 32):
+  rocprofv3 --kernel-trace --output-format csv -d T -o run -- python3 bench.py --profile-tiles
+  rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_INSTS_VALU --output-format csv -d P -o run \
+      -- python3 bench.py --profile-tiles
+  python3 bench.py --mfma-summary T P
 """
 
 from __future__ import annotations
@@ -44,6 +50,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "breeze-tts-2_amd"))
 
 HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 matrix-core peak of MI355X
+MI355X_SIMDS = 256 * 4
+MI355X_CLOCK_GHZ = 2.4
 GROUP = 128
 EPS = 1e-6
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_int4_gateup_k2560_n20480_m1_traffic.txt")
@@ -94,9 +103,15 @@ def main() -> int:
                     help="only launch the gate|up GEMV (eagerly) and a 256 MiB copy, for counter runs")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarize two rocprofv3 --pmc runs of --profile-gateup")
+    ap.add_argument("--profile-tiles", action="store_true",
+                    help="only launch the several-row (C4, M = 16 and 32) GEMVs eagerly, for counter runs")
+    ap.add_argument("--mfma-summary", nargs=2, metavar=("TRACE_DIR", "PMC_DIR"),
+                    help="summarize a rocprofv3 --kernel-trace run and a --pmc run of --profile-tiles")
     args = ap.parse_args()
     if args.pmc_summary:
         return pmc_summary(*args.pmc_summary)
+    if args.mfma_summary:
+        return mfma_summary(*args.mfma_summary)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the decode GEMVs here run "
               "on a single MI355X and no multi-GPU path is built).", file=sys.stderr)
@@ -117,6 +132,8 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     log(f"device {torch.cuda.get_device_name(0)}")
+    if args.profile_tiles:
+        return profile_tiles(torch, G, dev)
 
     # ---- synthetic C2 weights (seed 0: W, then gamma, then x, on the CPU)
     K1, N1, K2, N2, M = 2560, 20480, 10240, 2560, 1
@@ -291,6 +308,92 @@ def main() -> int:
     return 0
 
 
+# The several-row GEMVs whose matrix-core use is reported (C4 at M = 16, 32,
+# tile_cases() in launch order), each launched TILE_REPS times (after one
+# sizing launch) by --profile-tiles.
+TILE_REPS = 20
+
+
+def tile_cases() -> list:
+    return [(name, fmt, N, K, M) for name, fmt, N, K, _, _, _ in CONFIG_SHAPES if name.startswith("C4")
+            for M in (16, 32)]
+
+
+def profile_tiles(torch, G, dev) -> int:
+    """Launch each tile_cases() GEMV TILE_REPS times (launch shape from the
+    static table or the built-in rule, as in the config table) for
+    rocprofv3 counter and trace runs; --mfma-summary reads them back."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    for name, fmt, N, K, M in tile_cases():
+        w = torch.randn(N, K, device=dev, generator=gen) * 0.02
+        if fmt == "int4":
+            p, sc = G.quantize_int4_device(w, GROUP, True, G.W_INT4_ZP)[:2]
+            wfmt = G.W_INT4_ZP
+        else:
+            c, sc = G.quantize_fp8_device(w, 1e-12)
+            p, wfmt = c.view(torch.uint8), G.W_FP8
+        del w
+        x = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
+        out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+        G.gemv(x, p, wfmt, N, sc0=sc, group=GROUP, out=out)  # sizes the workspace (one extra launch)
+        torch.cuda.synchronize()
+        for _ in range(TILE_REPS):
+            G.gemv(x, p, wfmt, N, sc0=sc, group=GROUP, out=out)
+        torch.cuda.synchronize()
+        log(f"{name} M={M}: {TILE_REPS + 1} launches")
+    return 0
+
+
+def mfma_summary(trace_dir: str, pmc_dir: str) -> int:
+    """Matrix-core utilisation of the several-row tile GEMVs: per launch,
+    SQ_VALU_MFMA_BUSY_CYCLES (summed over all SIMDs) / (SIMDs x launch
+    duration x peak engine clock), with the duration from the kernel trace
+    of the same command.  At a lower actual clock the utilisation is higher,
+    so this is a lower bound."""
+    import csv
+    import glob
+    import statistics
+
+    def rows(d, pattern):
+        paths = glob.glob(os.path.join(d, "**", pattern), recursive=True)
+        if not paths:
+            raise SystemExit(f"no {pattern} under {d}")
+        return list(csv.DictReader(open(paths[0])))
+
+    cases = tile_cases()
+
+    def groups(seq):
+        # launches of the tile kernel in launch order, split into the tile_cases() runs
+        n = TILE_REPS + 1
+        if len(seq) != n * len(cases):
+            raise SystemExit(f"{len(seq)} tile dispatches, expected {n * len(cases)}")
+        return [seq[i * n + 1:(i + 1) * n] for i in range(len(cases))]
+
+    tr = sorted((int(r["Dispatch_Id"]), int(r["End_Timestamp"]) - int(r["Start_Timestamp"]), r["Kernel_Name"])
+                for r in rows(trace_dir, "*kernel_trace.csv") if "gemv_tile" in r["Kernel_Name"])
+    per = {}
+    for r in rows(pmc_dir, "*counter_collection.csv"):
+        if "gemv_tile" not in r["Kernel_Name"]:
+            continue
+        per.setdefault(int(r["Dispatch_Id"]), {}).setdefault(r["Counter_Name"], 0.0)
+        per[int(r["Dispatch_Id"])][r["Counter_Name"]] += float(r["Counter_Value"])
+    pm = [per[k] for k in sorted(per)]
+    print(f"matrix-core use of the several-row tile GEMVs, MI355X ({MI355X_SIMDS} SIMDs, "
+          f"{MI355X_CLOCK_GHZ} GHz peak engine clock); median of {TILE_REPS} launches each")
+    print(f"{'config':28s} {'M':>3s} {'us':>7s} {'TFLOP/s':>8s} {'MFMA busy':>10s} {'util':>7s} "
+          f"{'MFMA instr':>10s} {'VALU instr':>11s}  kernel")
+    for (name, fmt, N, K, M), t, c in zip(cases, groups(tr), groups(pm)):
+        us = statistics.median(d for _, d, _ in t) / 1e3
+        busy = statistics.median(x.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) for x in c)
+        util = busy / (MI355X_SIMDS * us * 1e-6 * MI355X_CLOCK_GHZ * 1e9)
+        kern = re.search(r"gemv_tile<[^>]*>", t[0][2])
+        print(f"{name:28s} {M:3d} {us:7.2f} {2.0 * M * N * K / us / 1e6:8.1f} {busy:10.0f} {100 * util:6.2f}% "
+              f"{statistics.median(x.get('SQ_INSTS_MFMA', 0.0) for x in c):10.0f} "
+              f"{statistics.median(x.get('SQ_INSTS_VALU', 0.0) for x in c):11.0f}  {kern.group(0) if kern else ''}")
+    return 0
+
+
 def pmc_summary(fetch_dir: str, write_dir: str) -> int:
     """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the gate|up GEMV from
     two rocprofv3 counter runs of --profile-gateup, each scaled by the ratio
@@ -356,6 +459,7 @@ def config_table(torch, G, dev, log) -> list:
     or fp8 e4m3 per-row, bf16 x N(0, 1)), timed as HIP-graph replays over
     weight copies rotating through >= 1 GiB: µs per call, algorithmic GB/s
     and the fraction of the 8 TB/s bytes-moved roofline."""
+    from breeze_amd import tuning
     from breeze_amd.fused.kernels import graph_time_us
 
     gen = torch.Generator(device=dev)
@@ -390,8 +494,12 @@ def config_table(torch, G, dev, log) -> list:
             us = graph_time_us(call, iters=2 * ncopy)
             nbytes = algo_bytes(bits, N, K, M, norm, epi)
             roof = nbytes / HBM_PEAK_GBPS / 1e3
+            tflops = 2.0 * M * N * K / us / 1e6
+            launch = tuning.lookup(dev, N, K, wfmt, epi, norm, M)
             rows.append({"config": name, "M": M, "us": round(us, 2), "gbps": round(nbytes / us / 1e3, 1),
-                         "roofline_us": round(roof, 2), "frac": round(roof / us, 3)})
+                         "roofline_us": round(roof, 2), "frac": round(roof / us, 3),
+                         "tflops": round(tflops, 2), "mfma_peak_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 5),
+                         "launch": list(launch) if launch else "rule"})
             log(f"{name:42s} M={M:2d}: {us:7.2f} us  {nbytes / us / 1e3:6.0f} GB/s  "
                 f"({roof / us * 100:4.1f}% of roofline)")
         del copies

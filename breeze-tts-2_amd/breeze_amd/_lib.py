@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede loading the HIP library)
 
 LIB_PATH = Path(os.environ.get("BZ_LIB", str(Path(__file__).resolve().parent / "libbzgemv.so")))
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # enums of include/bz_gemv.h
 OK = 0
@@ -60,6 +60,7 @@ class GemvDesc(ctypes.Structure):
         ("cfg_waves", ctypes.c_int32),
         ("cfg_tiles", ctypes.c_int32),
         ("cfg_path", ctypes.c_int32),
+        ("cfg_slices", ctypes.c_int32),
         ("eps", ctypes.c_float),
         ("x", ctypes.c_void_p),
         ("ldx", ctypes.c_int64),

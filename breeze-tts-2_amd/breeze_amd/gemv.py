@@ -89,13 +89,13 @@ def gemv(
     residual: Optional[torch.Tensor] = None,
     out: Optional[torch.Tensor] = None,
     out_dtype: torch.dtype = torch.bfloat16,
-    cfg: tuple = (0, 0, 0, 0),
+    cfg: tuple = (0, 0, 0, 0, 0),
 ) -> torch.Tensor:
     """out[M, N_out] = epilogue(rmsnorm?(x) @ w_eff^T) in one launch.
 
-    ``cfg`` (depth, waves, tiles, path) all zero takes the static per-arch
-    table's launch shape for this GEMV if it has one (tuning.py), else the
-    library's built-in rule.
+    ``cfg`` (depth, waves, tiles, path[, slices]) all zero takes the static
+    per-arch table's launch shape for this GEMV if it has one (tuning.py),
+    else the library's built-in rule.
 
     x [M, K] (any float dtype; computed as bf16), weight of format ``wfmt``
     with ``n`` rows, optional RMSNorm gamma [K], epilogue NONE / SILU_GATE
@@ -143,10 +143,12 @@ def gemv(
     d.epilogue = epilogue
     d.out_dtype = _DT[out.dtype]
     d.residual_dtype = res_dt
-    cfg = (tuple(cfg) + (0, 0, 0, 0))[:4]
-    if cfg == (0, 0, 0, 0):
-        cfg = _tuning.lookup(dev, n, K, wfmt, epilogue, gamma is not None, M) or cfg
-    d.cfg_depth, d.cfg_waves, d.cfg_tiles, d.cfg_path = cfg
+    cfg = (tuple(cfg) + (0, 0, 0, 0, 0))[:5]
+    if cfg == (0, 0, 0, 0, 0):
+        found = _tuning.lookup(dev, n, K, wfmt, epilogue, gamma is not None, M)
+        if found:
+            cfg = (tuple(found) + (0, 0, 0, 0, 0))[:5]
+    d.cfg_depth, d.cfg_waves, d.cfg_tiles, d.cfg_path, d.cfg_slices = cfg
     d.eps = eps
     d.x, d.ldx = x.data_ptr(), x.stride(0)
     d.w = w.data_ptr()

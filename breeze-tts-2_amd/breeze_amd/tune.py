@@ -5,12 +5,13 @@
 Run once per GPU architecture (the reference instead tunes at install time,
 models/fused/kernels.py:262-286, and persists per GPU name, :289-331).  Each
 decode GEMV shape of the reference's models and of the benchmark
-configurations is timed at M = 1 and 2 as HIP-graph replays over rotating
-weight copies (so the weights stream from HBM, not the 256 MB Infinity
-Cache), for the built-in rule and a grid of (depth, waves, tiles, path);
-an entry is written only where the best shape beats the built-in rule by at
-least --min-gain.  Every candidate is validated against the built-in rule's
-output before it is timed.
+configurations is timed at M = 1 and 2, and the several-row shapes at
+M = 4..32, as HIP-graph replays over rotating weight copies (so the weights
+stream from HBM, not the 256 MB Infinity Cache), for the built-in rule and a
+grid of (depth, waves, tiles, path[, slices]); an entry is written only where
+the best shape beats the built-in rule by at least --min-gain.  Every
+candidate is validated against the built-in rule's output before it is
+timed.
 """
 
 from __future__ import annotations
@@ -46,6 +47,19 @@ SHAPES = [
 
 CANDIDATES = [c for c in itertools.product((2, 4, 8), (4, 8), (0, 2), (1, 2, 3))]
 
+# Several-row GEMVs (MTP draft verification + CFG, M = 4..32) of the
+# benchmark's large-M configuration: no prologue or epilogue.  Candidates: the
+# row-sliced matrix-core paths' built-in shapes and the tile kernel's
+# (depth, waves, tiles, 4, slices) grid.
+ROW_SHAPES = [
+    ("C4 int4 up", "int4", 20480, 2560), ("C4 int4 down", "int4", 2560, 10240),
+    ("C4 fp8 up", "fp8", 20480, 2560), ("C4 fp8 down", "fp8", 2560, 10240),
+]
+ROW_MS = (4, 8, 16, 32)
+ROW_CANDIDATES = [(0, 0, 0, 2), (0, 0, 0, 3)] + [
+    (d, w, t, 4, n) for d, w, t, n in itertools.product((2, 4, 8), (4, 8), (1, 2), (0, 1, 2, 3, 4, 6, 8, 12, 16))
+]
+
 
 def _weights(fmt, N, K, dev):
     w = torch.randn(N, K, device=dev) * 0.02
@@ -63,11 +77,13 @@ def sweep(budget_mb: int, min_gain: float, log=print) -> dict:
     dev = torch.device("cuda", torch.cuda.current_device())
     arch = tuning.arch_of(dev)
     table = {}
-    for name, fmt, N, K, epi, norm in SHAPES:
+    jobs = [(name, fmt, N, K, epi, norm, (1, 2), CANDIDATES) for name, fmt, N, K, epi, norm in SHAPES]
+    jobs += [(name, fmt, N, K, 0, False, ROW_MS, ROW_CANDIDATES) for name, fmt, N, K in ROW_SHAPES]
+    for name, fmt, N, K, epi, norm, Ms, candidates in jobs:
         base, wbytes = _weights(fmt, N, K, dev)
         ncopy = max(2, -(-(budget_mb << 20) // wbytes))
         copies = [{k: (v.clone() if torch.is_tensor(v) else v) for k, v in base.items()} for _ in range(ncopy)]
-        for M in (1, 2):
+        for M in Ms:
             x = torch.randn(M, K, device=dev).to(torch.bfloat16)
             gamma = (1 + 0.1 * torch.randn(K, device=dev)).to(torch.bfloat16) if norm else None
             n_out = N // 2 if epi == G.EPI_SILU_GATE else N
@@ -79,7 +95,7 @@ def sweep(budget_mb: int, min_gain: float, log=print) -> dict:
                 w, wf = a.pop("w"), a.pop("wfmt")
                 return G.gemv(x, w, wf, N, gamma=gamma, epilogue=epi, residual=res, out=o, cfg=cfg, **a)
 
-            ref = run((0, 0, 0, 0), o=torch.empty_like(out)).float()
+            ref = run((0, 0, 0, 0, 0), o=torch.empty_like(out)).float()
 
             def timed(cfg):
                 st = {"i": 0}
@@ -91,9 +107,9 @@ def sweep(budget_mb: int, min_gain: float, log=print) -> dict:
                 return graph_time_us(fn, iters=min(2 * ncopy, 64))
 
             tuning._TABLES[arch] = {}  # time the built-in rule, not an older table
-            t_auto = timed((0, 0, 0, 0))
+            t_auto = timed((0, 0, 0, 0, 0))
             best = (t_auto, None)
-            for cfg in CANDIDATES:
+            for cfg in candidates:
                 try:
                     got = run(cfg, o=torch.empty_like(out)).float()
                 except RuntimeError:

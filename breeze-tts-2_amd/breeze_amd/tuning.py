@@ -10,8 +10,9 @@ better launch shape.  The table ships with the package
 time, so a call stays capture-safe and reentrant.
 
 Key: "<arch>|N|K|wfmt|epilogue|norm|M-bucket" (M-bucket = M rounded up to
-1, 2, 4, 8, 16 or 32), value: [depth, waves, tiles, path] as in
-bz_gemv_desc's cfg fields.
+1, 2, 4, 8, 16 or 32; larger M takes the 32 bucket), value: [depth, waves,
+tiles, path] or [depth, waves, tiles, path, slices] as in bz_gemv_desc's
+cfg fields.
 """
 
 from __future__ import annotations

@@ -89,7 +89,7 @@ static int check_desc(const bz_gemv_desc* d, DescInfo& di) {
         if (!aligned(d->sc0, 2) || !aligned(d->sc1, 2)) return BZ_ERR_ALIGNMENT;
     }
     if (!aligned(d->out, d->out_dtype == BZ_DT_F32 ? 4 : 2)) return BZ_ERR_ALIGNMENT;
-    if (d->cfg_path < 0 || d->cfg_path > PATH_TILE) return BZ_ERR_INVALID_ARG;
+    if (d->cfg_path < 0 || d->cfg_path > PATH_TILE || d->cfg_slices < 0) return BZ_ERR_INVALID_ARG;
     di.n_out = n_out;
     di.glog2 = glog2;
     di.row_bytes = row_bytes;
@@ -99,14 +99,16 @@ static int check_desc(const bz_gemv_desc* d, DescInfo& di) {
 
 // Launch shape of the several-row tile kernel (bz_gemv_tile.h).
 struct TilePlan {
-    int MB, T, D, ks, nsl, ncb;
+    int MB, T, D, nw, ks, nsl, ncb;
     size_t lds, ws;
 };
 
 // x slice bytes the automatic rule allows per workgroup (two workgroups per
-// CU fit the 160 KB of LDS), and the workgroups it aims for (two per CU).
-constexpr int kTileXBudget = 64 * 1024;
-constexpr int kTileTargetWorkgroups = 512;
+// CU fit the 160 KB of LDS), and the fewest workgroups it aims for: with 8
+// waves each, measured on MI355X (C4 shapes, M = 8..32) the best slice counts
+// give 160-240 workgroups; more slices only add split-K partials.
+constexpr int kTileXBudget = 80 * 1024 - 512;
+constexpr int kTileTargetWorkgroups = 192;
 
 // BZ_OK and the plan of one launch over M <= kTileMaxRows rows when the tile
 // kernel can run this descriptor (its cfg_* fields are read when cfg_path
@@ -118,17 +120,22 @@ static int tile_plan(const bz_gemv_desc* d, const DescInfo& di, int M, TilePlan&
     if (d->gamma || d->epilogue == BZ_EPI_SILU_GATE) return BZ_ERR_UNSUPPORTED;
     const int UK = mfma_unit_k(wf);
     if ((di.i4 && d->group < 128) || K % UK || di.row_bytes >= (1 << 24)) return BZ_ERR_UNSUPPORTED;
+    // 32-bit offsets inside the kernel: x rows of a launch, a slice of partials
+    if ((int64_t)M * d->ldx >= (int64_t(1) << 31) || (int64_t)M * di.n_out >= (int64_t(1) << 31))
+        return BZ_ERR_UNSUPPORTED;
     pl.MB = (M + 15) / 16;
     pl.T = forced && d->cfg_tiles ? d->cfg_tiles : 1;
     pl.D = forced && d->cfg_depth ? d->cfg_depth : 4;
-    if ((pl.T != 1 && pl.T != 2) || (pl.D != 2 && pl.D != 4 && pl.D != 8)) return BZ_ERR_INVALID_ARG;
-    const int cbw = kTileWaves * 16 * pl.T;
+    pl.nw = forced && d->cfg_waves ? d->cfg_waves : 8;
+    if ((pl.T != 1 && pl.T != 2) || (pl.D != 2 && pl.D != 4 && pl.D != 8) || (pl.nw != 4 && pl.nw != 8))
+        return BZ_ERR_INVALID_ARG;
+    const int cbw = pl.nw * 16 * pl.T;
     pl.ncb = (di.n_out + cbw - 1) / cbw;
     if (pl.ncb > kTileCounters) return BZ_ERR_UNSUPPORTED;
     const int units = K / UK;
     int nsl;
-    if (forced && d->cfg_waves) {
-        nsl = d->cfg_waves;
+    if (forced && d->cfg_slices) {
+        nsl = d->cfg_slices;
     } else {
         const int want = (kTileTargetWorkgroups + pl.ncb - 1) / pl.ncb;
         const int max_units = std::max(1, (kTileXBudget / (2 * M) - 8) / UK);
@@ -241,6 +248,7 @@ extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
                 l.MB = q.MB;
                 l.T = q.T;
                 l.D = q.D;
+                l.nw = q.nw;
                 l.lds = q.lds;
                 l.grid = (unsigned)(q.ncb * q.nsl);
                 const int rc = launch_tile(wf, tp, l, st);

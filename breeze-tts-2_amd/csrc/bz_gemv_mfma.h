@@ -57,10 +57,11 @@ __host__ __device__ inline MfmaLds mfma_lds_layout(int M, int T, int NW, int K, 
     return L;
 }
 
-// Sum over each aligned group of 16 lanes; every lane of the group gets it.
+// Sum over each aligned group of 16 lanes (one DPP row); every lane of the
+// group gets it.  row_ror:8 pairs lane i with lane i ^ 8 of the same row.
 __device__ __forceinline__ float sum16(float v) {
     v = sum8(v);
-    return v + __shfl_xor(v, 8, 64);
+    return v + dpp_f32<0x128>(v);
 }
 
 // Stage one 8-element block of x (natural block order; int4 blocks are

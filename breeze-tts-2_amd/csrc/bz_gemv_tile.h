@@ -5,7 +5,8 @@
 // The row-sliced streaming kernels (bz_gemv_mfma.h, bz_gemv_i8.h) hold at
 // most 4 rows of x per launch (16 on the int8 path for rows of <= 4096 k), so
 // 16 or 32 rows re-stream the weights 2-8 times.  Here a workgroup owns a
-// column block (4 waves x T tiles of 16 output columns) and one K slice:
+// column block (NW = 4 or 8 waves x T tiles of 16 output columns) and one K
+// slice:
 //   * grid = column blocks x K slices; block b takes column block b / nsl and
 //     slice b % nsl, so the slices of one column block run back to back and
 //     its last arrival finds the partials recently written;
@@ -37,8 +38,7 @@
 
 namespace bz {
 
-constexpr int kTileThreads = 256;
-constexpr int kTileWaves = kTileThreads / 64;
+constexpr int kTileMaxThreads = 512;  // 8 waves
 constexpr int kTileXB = 8;            // 16-byte blocks of x per thread loaded ahead of the weights
 constexpr int kTileCounters = 4096;   // column blocks per launch (counters at the workspace start)
 constexpr size_t kTilePartOffset = (size_t)kTileCounters * 4;
@@ -54,7 +54,7 @@ struct TileParams {
 };
 
 struct TileLaunch {
-    int MB, T, D;
+    int MB, T, D, nw;
     size_t lds;
     unsigned grid;
 };
@@ -114,11 +114,12 @@ __device__ __forceinline__ void tile_store(const GemvParams& p, float v, int r, 
 }
 
 template <int WF, int MB, int T, int D>
-__global__ void __launch_bounds__(kTileThreads) gemv_tile(TileParams tp) {
+__global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const GemvParams& p = tp.p;
     constexpr int UK = mfma_unit_k(WF);
     constexpr int RS = 16 * MB;  // x128 row stride (rows per unit)
+    const int nthr = blockDim.x, NW = nthr >> 6;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 15, kb = lane >> 4;
@@ -128,7 +129,7 @@ __global__ void __launch_bounds__(kTileThreads) gemv_tile(TileParams tp) {
     const int kl = min(tp.ks, p.K - k0);  // host: a multiple of UK, > 0
     const int nu = kl / UK;
     const int xrow = tile_xrow(tp.ks);
-    const int col0 = (cb * kTileWaves + wave) * 16 * T;  // wave-uniform
+    const int col0 = (cb * NW + wave) * 16 * T;  // wave-uniform
     const bool active = col0 < p.n_out;
 
     const TileLds L = tile_lds_layout(M, MB, tp.ks, WF);
@@ -136,14 +137,31 @@ __global__ void __launch_bounds__(kTileThreads) gemv_tile(TileParams tp) {
     float* x128 = reinterpret_cast<float*>(smem + L.x128);
     int& last_arrival = *reinterpret_cast<int*>(smem + L.flag);
 
-    // 0. the first blocks of the x slice (indices clamped: straight-line loads)
-    const int nblk = kl >> 3, total = M * nblk;
+    // 0. the first blocks of the x slice.  Block tid + nthr i is row m, block
+    //    kq of that row; (m, kq) advance by a uniform step, so there is one
+    //    division per thread.  Rows past the end load row M-1 (never staged):
+    //    the loads stay straight-line.
+    const int nblk = kl >> 3;
+    const int dm = nthr / nblk, dk = nthr - dm * nblk;
+    const int m_first = tid / nblk, kq_first = tid - m_first * nblk;
+    const uint16_t* xb = p.x + k0;
+    const int ldx = (int)p.ldx;  // host: M * ldx < 2^31
+    auto advance = [&](int& m, int& kq) {
+        kq += dk;
+        m += dm;
+        if (kq >= nblk) {
+            kq -= nblk;
+            ++m;
+        }
+    };
     u32x4 xr[kTileXB];
+    {
+        int m = m_first, kq = kq_first;
 #pragma unroll
-    for (int i = 0; i < kTileXB; ++i) {
-        const int bi = min(tid + i * kTileThreads, total - 1);
-        const int m = bi / nblk;
-        xr[i] = ldg16(p.x + (int64_t)m * p.ldx + k0 + (bi - m * nblk) * 8);
+        for (int i = 0; i < kTileXB; ++i) {
+            xr[i] = ldg16(xb + min(m, M - 1) * ldx + kq * 8);
+            advance(m, kq);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -152,26 +170,27 @@ __global__ void __launch_bounds__(kTileThreads) gemv_tile(TileParams tp) {
     uint32_t scb[D][T];
     const int ub0 = k0 / UK;
     uint32_t loff[T];  // lane offset inside the tile: row (clamped to the last column) and 16-byte slot
+    uint32_t soff[T];  // int4: the lane's row in the scale arrays ([G][N] pairs, or [N][G])
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         const int lr = min(j, max(p.n_out - 1 - (col0 + 16 * t), 0));
         loff[t] = __umul24((uint32_t)lr, (uint32_t)p.row_bytes) + (uint32_t)(kb * 16);
+        const int row = min(col0 + 16 * t + j, p.n_out - 1);
+        soff[t] = WF == WF_I4ZP ? (uint32_t)row : (uint32_t)row * (uint32_t)p.G;
     }
     auto issue = [&](int d, StepCursor c) {
         const int u = ub0 + c.ch;
+        const int g = (u * 128) >> p.glog2;  // one group per unit (group >= 128)
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int ct = min(col0 + 16 * t, p.n_out - 1);
             const uint8_t* base = p.w + (int64_t)ct * p.row_bytes + (int64_t)u * 64;  // uniform
             buf[d][t] = ldg16(base + loff[t]);
-            if (is_int4(WF)) {
-                const int row = min(col0 + 16 * t + j, p.n_out - 1);
-                const int g = (u * 128) >> p.glog2;
-                if (WF == WF_I4ZP)
-                    scb[d][t] = reinterpret_cast<const uint32_t*>(p.sc0)[(int64_t)g * p.N + row];
-                else
-                    scb[d][t] = (uint32_t)reinterpret_cast<const uint16_t*>(p.sc0)[(int64_t)row * p.G + g] |
-                                ((uint32_t)reinterpret_cast<const uint16_t*>(p.sc1)[(int64_t)row * p.G + g] << 16);
+            if (WF == WF_I4ZP) {
+                scb[d][t] = (reinterpret_cast<const uint32_t*>(p.sc0) + (int64_t)g * p.N)[soff[t]];
+            } else if (WF == WF_I4MIN) {
+                scb[d][t] = (uint32_t)(reinterpret_cast<const uint16_t*>(p.sc0) + g)[soff[t]] |
+                            ((uint32_t)(reinterpret_cast<const uint16_t*>(p.sc1) + g)[soff[t]] << 16);
             }
         }
     };
@@ -179,18 +198,17 @@ __global__ void __launch_bounds__(kTileThreads) gemv_tile(TileParams tp) {
     if (active) pipeline_prime<0, D>(nu, 1, nu, 0, ic, issue);
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. stage x (the rest of the slice is loaded here, behind the weights)
+    // 2. stage x (the rest of the slice is loaded here, behind the weights).
+    //    m < M is uniform over each aligned 16-lane group for int4 (nblk is
+    //    a multiple of 16), as the unit sums need.
+    {
+        int m = m_first, kq = kq_first;
 #pragma unroll
-    for (int i = 0; i < kTileXB; ++i) {
-        const int bi = tid + i * kTileThreads;
-        if (bi < total) {  // uniform over each 16-lane group (total % 16 == 0 for int4)
-            const int m = bi / nblk;
-            tile_stage<WF>(xr[i], m, bi - m * nblk, xs, x128, xrow, RS);
+        for (int i = 0; i < kTileXB; ++i) {
+            if (m < M) tile_stage<WF>(xr[i], m, kq, xs, x128, xrow, RS);
+            advance(m, kq);
         }
-    }
-    for (int bi = tid + kTileXB * kTileThreads; bi < total; bi += kTileThreads) {
-        const int m = bi / nblk, kq = bi - m * nblk;
-        tile_stage<WF>(ldg16(p.x + (int64_t)m * p.ldx + k0 + kq * 8), m, kq, xs, x128, xrow, RS);
+        for (; m < M; advance(m, kq)) tile_stage<WF>(ldg16(xb + m * ldx + kq * 8), m, kq, xs, x128, xrow, RS);
     }
     __syncthreads();
 
@@ -288,8 +306,11 @@ __global__ void __launch_bounds__(kTileThreads) gemv_tile(TileParams tp) {
         return;
     }
 
-    // 4b. several slices: partials, arrival, and the last arrival's sum
+    // 4b. several slices: partials, arrival, and the last arrival's sum.
+    //    Partial offsets inside a slice are 32-bit (M * N_out < 2^31).
+    const int64_t sstride = (int64_t)M * p.n_out;
     if (active) {
+        float* ps = tp.part + sl * sstride;  // uniform
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int c = col0 + 16 * t + j;
@@ -300,8 +321,8 @@ __global__ void __launch_bounds__(kTileThreads) gemv_tile(TileParams tp) {
                 for (int q = 0; q < 4; ++q) {
                     const int r = 16 * mb + 4 * kb + q;
                     if (r < M)
-                        __hip_atomic_store(tp.part + ((int64_t)sl * M + r) * p.n_out + c, acc[t][mb][q],
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(ps + (r * p.n_out + c), acc[t][mb][q], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
                 }
         }
     }
@@ -313,35 +334,40 @@ __global__ void __launch_bounds__(kTileThreads) gemv_tile(TileParams tp) {
     }
     __syncthreads();
     if (!last_arrival) return;
-    constexpr int CBW = kTileWaves * 16 * T;  // columns of a block
+    // Each thread sums 4 outputs, 4 slices of each in flight per batch;
+    // slices are added in slice order.
+    const int CBW = NW * 16 * T;  // columns of a block (a power of two)
+    const int cbw_log2 = __builtin_ctz(CBW);
     const int nout = M * CBW;
-    for (int i0 = 0; i0 < nout; i0 += 4 * kTileThreads) {
+    for (int i0 = 0; i0 < nout; i0 += 4 * nthr) {
         float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int s0 = 0; s0 < nsl; s0 += 8) {
-            float v[4][8];
+        int off[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int i = min(i0 + tid + q * kTileThreads, nout - 1);
-                const int r = i / CBW;
-                const int c = min(cb * CBW + (i - r * CBW), p.n_out - 1);
+        for (int q = 0; q < 4; ++q) {
+            const int i = min(i0 + tid + q * nthr, nout - 1);
+            const int r = i >> cbw_log2;
+            off[q] = r * p.n_out + min(cb * CBW + (i - r * CBW), p.n_out - 1);
+        }
+        for (int s0 = 0; s0 < nsl; s0 += 4) {
+            float v[4][4];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int s = min(s0 + u, nsl - 1);
-                    v[q][u] = __hip_atomic_load(tp.part + ((int64_t)s * M + r) * p.n_out + c, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-                }
+            for (int u = 0; u < 4; ++u) {
+                const float* ps = tp.part + min(s0 + u, nsl - 1) * sstride;  // uniform
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    v[q][u] = __hip_atomic_load(ps + off[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q)
 #pragma unroll
-                for (int u = 0; u < 8; ++u)
+                for (int u = 0; u < 4; ++u)
                     if (s0 + u < nsl) sum[q] += v[q][u];
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const int i = i0 + tid + q * kTileThreads;
+            const int i = i0 + tid + q * nthr;
             if (i >= nout) continue;
-            const int r = i / CBW;
+            const int r = i >> cbw_log2;
             const int c = cb * CBW + (i - r * CBW);
             if (c < p.n_out) tile_store<WF>(p, sum[q], r, c);
         }
@@ -361,7 +387,7 @@ int launch_tile_kernel(const TileParams& tp, const TileLaunch& l, hipStream_t st
             raised.store(true, std::memory_order_relaxed);
         }
     }
-    hipLaunchKernelGGL(kern, dim3(l.grid), dim3(kTileThreads), l.lds, st, tp);
+    hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, tp);
     return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }
 

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define BZ_ABI_VERSION 1
+#define BZ_ABI_VERSION 2
 
 typedef enum bz_status {
     BZ_OK = 0,
@@ -95,9 +95,9 @@ typedef enum bz_dtype {
  * Used by tuning sweeps.
  *
  * Several rows (path 4).  Up to 32 rows of x per launch stream every weight
- * byte once: a workgroup owns 64 * cfg_tiles output columns (cfg_tiles 1 or
- * 2) and one K slice, and cfg_waves (path 4 only) sets the number of K
- * slices (0: about 512 workgroups, x slice <= 64 KB of LDS).  It needs no
+ * byte once: a workgroup of cfg_waves waves (4 or 8) owns 16 * cfg_tiles
+ * output columns per wave (cfg_tiles 1 or 2) and one of cfg_slices K slices
+ * (0: the built-in rule, x slice <= 80 KB of LDS).  It needs no
  * RMSNorm (gamma NULL), epilogue NONE or RESIDUAL, an int4 group >= 128 and
  * K a multiple of 128 (int4), 64 (fp8) or 32 (bf16); larger M runs 32 rows
  * per launch.  With more than one K slice the slices' fp32 partials go to
@@ -117,6 +117,7 @@ typedef struct bz_gemv_desc {
     int32_t out_dtype;        /* bz_dtype */
     int32_t residual_dtype;   /* bz_dtype */
     int32_t cfg_depth, cfg_waves, cfg_tiles, cfg_path;  /* 0 = automatic */
+    int32_t cfg_slices;       /* path 4: K slices (0 = automatic) */
     float eps;
     const void* x;  int64_t ldx;
     const void* w;

@@ -160,8 +160,8 @@ def test_workspace_sizes(L):
     assert ws(M=8, gamma=1 << 20) == 0
     assert ws(M=8, N=128, epilogue=1) == 0
     assert ws(M=8, abi_version=99) == 0
-    assert ws(M=2, cfg_path=4, cfg_waves=1) == 0               # one slice: no partials
-    assert ws(M=2, cfg_path=4, cfg_waves=2) == 16384 + 2 * 2 * 64 * 4
+    assert ws(M=2, cfg_path=4, cfg_slices=1) == 0              # one slice: no partials
+    assert ws(M=2, cfg_path=4, cfg_slices=2) == 16384 + 2 * 2 * 64 * 4
 
 
 @pytest.mark.parametrize(
@@ -171,6 +171,8 @@ def test_workspace_sizes(L):
         ({"cfg_path": 4, "M": 8}, "ERR_INVALID_ARG"),                       # split-K needs the workspace
         ({"cfg_path": 4, "M": 8, "workspace": 1 << 20, "workspace_bytes": 100}, "ERR_INVALID_ARG"),
         ({"cfg_path": 4, "M": 8, "cfg_tiles": 3}, "ERR_INVALID_ARG"),
+        ({"cfg_path": 4, "M": 8, "cfg_waves": 6}, "ERR_INVALID_ARG"),
+        ({"cfg_slices": -1}, "ERR_INVALID_ARG"),
         ({"cfg_path": 4, "M": 8, "cfg_depth": 16}, "ERR_INVALID_ARG"),
         ({"cfg_path": 4, "M": 8, "gamma": 1 << 20}, "ERR_UNSUPPORTED"),     # no RMSNorm prologue
         ({"cfg_path": 4, "M": 8, "N": 128, "epilogue": 1}, "ERR_UNSUPPORTED"),  # no SiLU gate

@@ -311,7 +311,9 @@ def test_errors_raise():
 
 
 @pytest.mark.parametrize("key", ["gfx950|1024|8192|2|2|0|1", "gfx950|2048|2048|0|2|0|2", "gfx950|4096|2048|3|0|1|1",
-                                 "gfx950|1536|1024|3|0|1|1"])
+                                 "gfx950|1536|1024|3|0|1|1", "gfx950|20480|2560|0|0|0|16", "gfx950|20480|2560|0|0|0|32",
+                                 "gfx950|2560|10240|0|0|0|32", "gfx950|20480|2560|2|0|0|8",
+                                 "gfx950|2560|10240|2|0|0|8"])
 def test_table_launch_shapes_match_oracle(key):
     """Entries of the committed launch-shape table, run through gemv()'s
     automatic selection, against the oracle."""

@@ -82,20 +82,21 @@ def test_tile_small(fmt, layout, M, nsl):
     N, K = SMALL[fmt]
     call, w_eff, rs = _case(fmt, N, K, seed=M + 3 * nsl, layout=layout)
     x = O.synth(8, K, M, seed=40 + M)[2]
-    _check(call(x, cfg=(0, nsl, 0, PATH)), x, w_eff, rs=rs)
+    _check(call(x, cfg=(0, 0, 0, PATH, nsl)), x, w_eff, rs=rs)
 
 
 @pytest.mark.parametrize("fmt", ["int4", "fp8", "bf16"])
-@pytest.mark.parametrize("depth,tiles,nsl", [(2, 1, 2), (8, 1, 5), (4, 2, 0), (8, 2, 7), (2, 2, 1), (4, 1, 64)])
-def test_tile_launch_shapes_residual(fmt, depth, tiles, nsl):
-    """Every (depth, tiles, slices) shape, residual epilogue, fp32 and bf16 out."""
+@pytest.mark.parametrize("depth,waves,tiles,nsl", [(2, 4, 1, 2), (8, 8, 1, 5), (4, 4, 2, 0), (8, 8, 2, 7), (2, 8, 2, 1),
+                                                   (4, 4, 1, 64), (4, 8, 1, 0)])
+def test_tile_launch_shapes_residual(fmt, depth, waves, tiles, nsl):
+    """Every (depth, waves, tiles, slices) shape, residual epilogue, fp32 and bf16 out."""
     N, K = SMALL[fmt]
     M = 20
     call, w_eff, rs = _case(fmt, N, K, seed=7)
     x = O.synth(8, K, M, seed=8)[2]
     res = _res(M, N, 9)
     for od in (torch.bfloat16, torch.float32):
-        got = call(x, G.EPI_RESIDUAL, res, cfg=(depth, nsl, tiles, PATH), out_dtype=od)
+        got = call(x, G.EPI_RESIDUAL, res, cfg=(depth, waves, tiles, PATH, nsl), out_dtype=od)
         _check(got, x, w_eff, O.EPI_RES, res, rs)
 
 
@@ -107,7 +108,7 @@ def test_tile_more_than_32_rows(fmt, M):
     call, w_eff, rs = _case(fmt, N, K, seed=11)
     x = O.synth(8, K, M, seed=12)[2]
     res = _res(M, N, 13)
-    _check(call(x, G.EPI_RESIDUAL, res, cfg=(0, 3, 0, PATH)), x, w_eff, O.EPI_RES, res, rs)
+    _check(call(x, G.EPI_RESIDUAL, res, cfg=(0, 0, 0, PATH, 3)), x, w_eff, O.EPI_RES, res, rs)
     _check(call(x, G.EPI_NONE, cfg=(0, 0, 0, 0)), x, w_eff, rs=rs)  # automatic rule
 
 
@@ -117,13 +118,13 @@ def test_tile_counters_reset_and_deterministic():
     the next call."""
     call, w_eff, _ = _case("int4", 200, 1280, seed=14)
     x = O.synth(8, 1280, 24, seed=15)[2]
-    first = call(x, cfg=(0, 5, 0, PATH)).clone()
+    first = call(x, cfg=(0, 0, 0, PATH, 5)).clone()
     _check(first, x, w_eff)
     call2, w2, rs2 = _case("fp8", 136, 1088, seed=16)
     x2 = O.synth(8, 1088, 9, seed=17)[2]
-    _check(call2(x2, cfg=(0, 17, 0, PATH)), x2, w2, rs=rs2)
+    _check(call2(x2, cfg=(0, 0, 0, PATH, 17)), x2, w2, rs=rs2)
     for _ in range(3):
-        again = call(x, cfg=(0, 5, 0, PATH))
+        again = call(x, cfg=(0, 0, 0, PATH, 5))
         assert torch.equal(again, first)
 
 
@@ -143,7 +144,7 @@ def test_tile_one_hot_int4_bit_exact():
     x[np.arange(len(ks)), ks] = 1.0
     for nsl in (1, 3, 8):
         got = f32(G.gemv(bf16_tensor(O.f32_to_bf16_bits(x)), d_w, G.W_INT4_ZP, N, sc0=d_sz, group=group,
-                         out_dtype=torch.float32, cfg=(0, nsl, 0, PATH)))
+                         out_dtype=torch.float32, cfg=(0, 0, 0, PATH, nsl)))
         for i, k in enumerate(ks):
             assert np.array_equal(got[i], w_eff[:, k]), (nsl, k)
 
@@ -159,7 +160,7 @@ def test_tile_one_hot_fp8_bit_exact():
     x[np.arange(len(ks)), ks] = 1.0
     for nsl in (1, 4):
         got = f32(G.gemv(bf16_tensor(O.f32_to_bf16_bits(x)), u8_tensor(codes), G.W_FP8, N,
-                         sc0=torch.ones(N, device="cuda"), out_dtype=torch.float32, cfg=(0, nsl, 0, PATH)))
+                         sc0=torch.ones(N, device="cuda"), out_dtype=torch.float32, cfg=(0, 0, 0, PATH, nsl)))
         for i, k in enumerate(ks):
             assert np.array_equal(got[i], want[:, k]), (nsl, k)
 
@@ -186,6 +187,8 @@ def test_tile_path_rejects_what_it_cannot_run():
         call(x, cfg=(3, 0, 0, PATH))    # depth 3
     with pytest.raises(RuntimeError, match="invalid argument"):
         call(x, cfg=(0, 0, 3, PATH))    # 3 tiles per wave
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        call(x, cfg=(0, 5, 0, PATH))    # 5 waves per workgroup
 
 
 def test_tile_graph_replays_match_eager():
@@ -197,7 +200,7 @@ def test_tile_graph_replays_match_eager():
     out = torch.empty(16, 200, device="cuda", dtype=torch.bfloat16)
 
     def run():
-        G.gemv(x, c.d_packed, G.W_INT4_ZP, 200, sc0=c.d_sz, group=128, out=out, cfg=(0, 5, 0, PATH))
+        G.gemv(x, c.d_packed, G.W_INT4_ZP, 200, sc0=c.d_sz, group=128, out=out, cfg=(0, 0, 0, PATH, 5))
 
     run()
     torch.cuda.synchronize()
@@ -221,7 +224,8 @@ def test_tile_graph_replays_match_eager():
 @pytest.mark.parametrize("depth", [2, 4, 8])
 @pytest.mark.parametrize("tiles", [1, 2])
 @pytest.mark.parametrize("M", [8, 24])
-def test_tile_every_instance_steady_loop(fmt, depth, tiles, M):
+@pytest.mark.parametrize("waves", [4, 8])
+def test_tile_every_instance_steady_loop(fmt, depth, tiles, M, waves):
     """Every (depth, tiles, row blocks) instance with one slice of >= 16
     units, so the unrolled steady loop of the weight pipeline runs (the
     first unit comes from the prologue's loads).  Regression: the nibble
@@ -232,4 +236,4 @@ def test_tile_every_instance_steady_loop(fmt, depth, tiles, M):
     N, K = {"int4": (160, 2560), "fp8": (160, 1024), "bf16": (160, 512)}[fmt]
     call, w_eff, rs = _case(fmt, N, K, seed=30 + depth + tiles + M)
     x = O.synth(8, K, M, seed=31)[2]
-    _check(call(x, cfg=(depth, 1, tiles, PATH), out_dtype=torch.float32), x, w_eff, rs=rs)
+    _check(call(x, cfg=(depth, waves, tiles, PATH, 1), out_dtype=torch.float32), x, w_eff, rs=rs)

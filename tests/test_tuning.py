@@ -33,7 +33,14 @@ def test_committed_table_entries_are_valid_shapes():
     for key, cfg in table.items():
         arch, N, K, wfmt, epi, norm, mb = key.split("|")
         assert arch == "gfx950" and int(mb) in (1, 2, 4, 8, 16, 32)
-        depth, waves, tiles, path = cfg
-        assert depth in (2, 4, 8, 16) and 1 <= waves <= 8 and tiles >= 0 and path in (1, 2, 3)
+        assert len(cfg) in (4, 5)
+        depth, waves, tiles, path = cfg[:4]
+        # 0 = the built-in choice for that field
+        assert depth in (0, 2, 4, 8, 16) and 0 <= waves <= 8 and tiles >= 0 and path in (1, 2, 3, 4)
         if path == 3:
             assert int(wfmt) in (0, 1)  # int8 matrix-core path is for int4 weights only
+        if path == 4:  # several-row tile kernel: no prologue or SiLU gate, 4 or 8 waves, 1 or 2 tiles
+            assert norm == "0" and epi != "1" and waves in (0, 4, 8) and tiles in (0, 1, 2) and depth <= 8
+            assert len(cfg) == 5 and cfg[4] >= 0
+        else:
+            assert len(cfg) == 4 or cfg[4] == 0
