@@ -310,12 +310,17 @@ def test_errors_raise():
         G.gemv(torch.zeros(1, 128, dtype=torch.bfloat16, device=_dev()), w, G.W_INT4_ZP, 8, group=128)
 
 
-@pytest.mark.parametrize("key", ["gfx950|1024|8192|2|2|0|1", "gfx950|2048|2048|0|2|0|2", "gfx950|4096|2048|3|0|1|1",
-                                 "gfx950|1536|1024|3|0|1|1", "gfx950|20480|2560|0|0|0|16", "gfx950|20480|2560|0|0|0|32",
-                                 "gfx950|2560|10240|0|0|0|32", "gfx950|20480|2560|2|0|0|8",
-                                 "gfx950|2560|10240|2|0|0|8"])
+def _table_keys():
+    import json
+    from pathlib import Path
+
+    path = Path(__file__).resolve().parents[1] / "breeze-tts-2_amd" / "breeze_amd" / "tune_gfx950.json"
+    return sorted(json.loads(path.read_text()))
+
+
+@pytest.mark.parametrize("key", _table_keys())
 def test_table_launch_shapes_match_oracle(key):
-    """Entries of the committed launch-shape table, run through gemv()'s
+    """Every entry of the committed launch-shape table, run through gemv()'s
     automatic selection, against the oracle."""
     from breeze_amd import tuning
 
