@@ -173,6 +173,7 @@ def gemv(
 _TILE_MIN_ROWS = 5
 _PATH_TILE = 4
 _GEMV_WS: dict = {}
+_GEMV_WS_RETIRED: list = []  # outgrown workspaces: a captured graph may still point at one
 
 
 def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
@@ -181,7 +182,9 @@ def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
     same device must not run concurrently on different streams (as with the
     reference's cached split-K buffer, models/fused/kernels.py:179,192-198).  It
     must be sized before a graph capture: an eager call of the same shape
-    (the graphs' warm-up steps) does that."""
+    (the graphs' warm-up steps) does that.  An outgrown buffer is kept alive
+    for the process, since a graph captured earlier still uses it (its
+    counters are zero again once its last call has finished)."""
     key = dev.index if dev.index is not None else torch.cuda.current_device()
     buf = _GEMV_WS.get(key)
     if buf is None or buf.numel() * 4 < nbytes:
@@ -191,6 +194,8 @@ def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
                 "eagerly before capturing"
             )
         n = max(nbytes, 2 * (buf.numel() * 4 if buf is not None else 0), 1 << 20)
+        if buf is not None:
+            _GEMV_WS_RETIRED.append(buf)
         buf = torch.zeros(-(-n // 4), dtype=torch.int32, device=torch.device("cuda", key))
         _GEMV_WS[key] = buf
     return buf

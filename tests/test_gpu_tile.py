@@ -237,3 +237,40 @@ def test_tile_every_instance_steady_loop(fmt, depth, tiles, M, waves):
     call, w_eff, rs = _case(fmt, N, K, seed=30 + depth + tiles + M)
     x = O.synth(8, K, M, seed=31)[2]
     _check(call(x, cfg=(depth, waves, tiles, PATH, 1), out_dtype=torch.float32), x, w_eff, rs=rs)
+
+
+def test_tile_graph_survives_workspace_growth():
+    """A graph captured over the device's GEMV workspace keeps working after
+    a larger call has grown (replaced) that workspace: the outgrown buffer
+    stays alive."""
+    from breeze_amd import gemv as gemv_mod
+
+    c = Int4Case(O.synth(200, 1280, 1, seed=26)[0], 128)
+    x = bf16_tensor(O.synth(8, 1280, 16, seed=27)[2])
+    out = torch.empty(16, 200, device="cuda", dtype=torch.bfloat16)
+
+    def run():
+        G.gemv(x, c.d_packed, G.W_INT4_ZP, 200, sc0=c.d_sz, group=128, out=out, cfg=(0, 0, 0, PATH, 5))
+
+    run()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s), torch.cuda.graph(g, stream=s):
+        run()
+    torch.cuda.current_stream().wait_stream(s)
+    before = gemv_mod._GEMV_WS[torch.cuda.current_device()].data_ptr()
+    # a much larger split-K call grows the workspace
+    big = Int4Case(O.synth(2048, 2560, 1, seed=28)[0], 128)
+    xb = bf16_tensor(O.synth(8, 2560, 32, seed=29)[2])
+    need = G.gemv(xb, big.d_packed, G.W_INT4_ZP, 2048, sc0=big.d_sz, group=128, cfg=(0, 0, 0, PATH, 20))
+    torch.cuda.synchronize()
+    assert gemv_mod._GEMV_WS[torch.cuda.current_device()].data_ptr() != before
+    _check(need, O.synth(8, 2560, 32, seed=29)[2], big.w_zp)
+    for i in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
