@@ -22,8 +22,13 @@
 //            16) and B = 16 key rows; q is carried as bf16 hi + lo parts
 //            (two MFMAs, ~16 significant bits; an fp32 cache also splits k)
 //   softmax  online (running max m, sum l) per head, exp2-based
-//   p v      VALU: lane l owns D/64 consecutive columns of every head and
-//            reads each value row with one coalesced load
+//   p v      bf16 cache, D <= 256: v_mfma_f32_16x16x16_bf16 per 16-column
+//            tile, A = p (through LDS, as bf16 hi + lo), B = 4 value rows
+//            of one column, which lane (col, grp) loads directly (4 rows x
+//            D/16 contiguous columns) so no cross-lane transpose is needed;
+//            fp32 cache or D = 512: VALU, lane l owns D/64 consecutive
+//            columns of every head and reads each value row with one
+//            coalesced load
 // The waves' (m, l, acc) are merged through LDS in a fixed order.
 #include "bz_attn.h"
 #include "bz_device.h"
@@ -38,6 +43,17 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ f32x4_t mfma16(const u32x4 a, const u32x4 b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
                                                   c, 0, 0, 0);
+}
+
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// D = A B + C, 16x16x16: A[i][k] in lane i + 16 (k/4) element k%4, B[k][j]
+// in lane j + 16 (k/4) element k%4, D[i][j] in lane j + 16 (i/4) element i%4
+// (checked on the hardware).
+__device__ __forceinline__ f32x4_t mfma16k16(const u32x2 a, const u32x2 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, a), __builtin_bit_cast(bf16x4_t, b),
+                                                    c, 0, 0, 0);
 }
 
 __device__ __forceinline__ float ld_any(const void* p, bool f32, int64_t i) {
@@ -198,12 +214,19 @@ struct AttnParams {
 };
 
 // The registers of one 16-position block: key operands and raw value words.
+// MV (bf16 cache, D <= 256): p v on the matrix cores, and lane (col, grp)
+// holds value rows 4 grp .. 4 grp + 3 of the block at columns D/16 col ..
+// D/16 col + D/16 - 1 -- column D/16 col + c of those 4 rows is exactly the
+// B operand of the 16x16x16 MFMA of column tile c.  Otherwise (VALU p v)
+// lane l holds columns DL l .. DL l + DL - 1 of all 16 rows.
 template <int DL, bool F32C>
 struct KvBlock {
-    static constexpr int T = 2 * DL;                                // MFMA k-steps per key row
-    static constexpr int VW = F32C ? DL : (DL >= 2 ? DL / 2 : 1);   // value words per lane and row
+    static constexpr int T = 2 * DL;  // MFMA k-steps per key row
+    static constexpr bool MV = !F32C && DL <= 4;
+    static constexpr int VW = MV ? 2 * DL : (F32C ? DL : (DL >= 2 ? DL / 2 : 1));  // value words per row
+    static constexpr int VR = MV ? 4 : kBlk;                                     // value rows per lane
     u32x4 kh[T], kl[T];
-    uint32_t v[kBlk][VW];
+    uint32_t v[VR][VW];
     uint32_t mraw;  // raw mask entry at this lane's key position
 };
 
@@ -280,9 +303,26 @@ __device__ __forceinline__ void load_block(const AttnParams& a, int64_t kv_base,
     const char* krow = kc + (int64_t)kpos * (D * ES) + 8 * grp * ES;
     for (int t = 0; t < KvBlock<DL, F32C>::T; ++t) load_k8<F32C>(krow, 32 * t, blk.kh[t], blk.kl[t]);
     const char* vc = static_cast<const char*>(a.vc) + kv_base * ES;
-    for (int p = 0; p < kBlk; ++p) {
-        const int row = min(s0 + p, last);
-        load_vraw<DL, F32C>(vc + (int64_t)row * (D * ES), DL * lane, blk.v[p]);
+    if constexpr (KvBlock<DL, F32C>::MV) {
+        for (int r = 0; r < 4; ++r) {
+            const int row = min(s0 + 4 * grp + r, last);
+            const uint16_t* vp = reinterpret_cast<const uint16_t*>(vc + (int64_t)row * (D * ES)) + 4 * DL * col;
+            if constexpr (DL == 1) {
+                const u32x2 t = *reinterpret_cast<const u32x2*>(vp);
+                blk.v[r][0] = t[0];
+                blk.v[r][1] = t[1];
+            } else {
+                for (int i = 0; i < DL / 2; ++i) {
+                    const u32x4 t = ldg16(vp + 8 * i);
+                    for (int e = 0; e < 4; ++e) blk.v[r][4 * i + e] = t[e];
+                }
+            }
+        }
+    } else {
+        for (int p = 0; p < kBlk; ++p) {
+            const int row = min(s0 + p, last);
+            load_vraw<DL, F32C>(vc + (int64_t)row * (D * ES), DL * lane, blk.v[p]);
+        }
     }
 }
 
@@ -316,11 +356,13 @@ __global__ void __launch_bounds__(kAttnThreads) attn_kernel(AttnParams a) {
     constexpr int T = D / 32;
     constexpr bool PF = !F32C && DL <= 4;  // prefetch the next block (registers allow it)
     using Blk = KvBlock<DL, F32C>;
+    constexpr bool MV = Blk::MV;          // p v on the matrix cores
+    constexpr int NT = D / 16;            // its column tiles
     __shared__ float qf[GM][D];
     __shared__ float css[(GM + 2) * DL];
     __shared__ float rinv[GM + 1];
     __shared__ u32x4 qop[T][2][64];  // the A operand (q hi, lo) of every lane
-    __shared__ float p_lds[kAttnWaves][kBlk][GM];
+    __shared__ float p_lds[kAttnWaves][kBlk * GM];  // MV: [head][position], else [position][head]
     __shared__ float st_m[kAttnWaves][GM], st_l[kAttnWaves][GM];
     __shared__ float wgt[kAttnWaves][GM], hm[GM], hl[GM];
     __shared__ float wsp[GM][BZ_ATTN_MAX_SPLIT];
@@ -475,11 +517,14 @@ __global__ void __launch_bounds__(kAttnThreads) attn_kernel(AttnParams a) {
         m[r] = kNegBig;
         l[r] = 0.0f;
     }
-    float acc[GM][DL];
+    float acc[GM][DL];  // VALU p v: head h, this lane's DL columns
     for (int h = 0; h < GM; ++h)
         for (int e = 0; e < DL; ++e) acc[h][e] = 0.0f;
+    f32x4_t accm[MV ? NT : 1];  // MV: tile c, lane (col, grp): heads 4 grp + r at column NT col + c
+    for (int c = 0; c < (MV ? NT : 1); ++c) accm[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // One block: scores on the matrix cores, online softmax, p v on the VALU.
+    // One block: scores on the matrix cores, online softmax, p v on the
+    // matrix cores (MV) or the VALU.
     auto process = [&](Blk& blk, const int s0) __attribute__((always_inline)) {
         const int kpos = s0 + col;
         const bool valid = kpos < s_hi;
@@ -501,11 +546,44 @@ __global__ void __launch_bounds__(kAttnThreads) attn_kernel(AttnParams a) {
             m[r] = mn;
             // every head slot of the block is written (rows past G hold
             // finite values of zero query rows and are never output)
-            if (4 * grp + r < GM) p_lds[wave][col][4 * grp + r] = pr;
+            if (4 * grp + r < GM) {
+                if constexpr (MV)
+                    p_lds[wave][(4 * grp + r) * kBlk + col] = pr;
+                else
+                    p_lds[wave][col * GM + 4 * grp + r] = pr;
+            }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if constexpr (MV) {
+            // A: head col's p at positions 4 grp .. 4 grp + 3 (rows from G
+            // on repeat head GM - 1 and are never output), as bf16 hi + lo
+            const float4 pq = *reinterpret_cast<const float4*>(&p_lds[wave][min(col, GM - 1) * kBlk + 4 * grp]);
+            const uint16_t h0 = f32_to_bf16(pq.x), h1 = f32_to_bf16(pq.y), h2 = f32_to_bf16(pq.z),
+                           h3 = f32_to_bf16(pq.w);
+            const u32x2 ah = {(uint32_t)h0 | ((uint32_t)h1 << 16), (uint32_t)h2 | ((uint32_t)h3 << 16)};
+            const u32x2 al = {pack_bf16x2(pq.x - bf16_to_f32(h0), pq.y - bf16_to_f32(h1)),
+                              pack_bf16x2(pq.z - bf16_to_f32(h2), pq.w - bf16_to_f32(h3))};
+            // the accumulator lane (col, grp) holds heads 4 grp + r: its own alphas
+            for (int c = 0; c < NT; ++c)
+                for (int r = 0; r < 4; ++r) accm[c][r] *= alpha[r];
+            for (int c = 0; c < NT; ++c) {
+                // B: column NT col + c of value rows 4 grp .. 4 grp + 3
+                const uint32_t w0 = blk.v[0][c >> 1], w1 = blk.v[1][c >> 1], w2 = blk.v[2][c >> 1],
+                               w3 = blk.v[3][c >> 1];
+                u32x2 bv;
+                if (c & 1) {
+                    bv[0] = (w0 >> 16) | (w1 & 0xFFFF0000u);
+                    bv[1] = (w2 >> 16) | (w3 & 0xFFFF0000u);
+                } else {
+                    bv[0] = (w0 & 0xFFFFu) | (w1 << 16);
+                    bv[1] = (w2 & 0xFFFFu) | (w3 << 16);
+                }
+                accm[c] = mfma16k16(ah, bv, accm[c]);
+                accm[c] = mfma16k16(al, bv, accm[c]);
+            }
+        } else {
         // rescale by head h's alpha (lane 16 (h / 4), element h % 4)
         for (int h = 0; h < GM; ++h) {
             const float al = bcast(alpha[h & 3], 16 * (h >> 2));
@@ -516,7 +594,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_kernel(AttnParams a) {
             for (int e = 0; e < DL; ++e) vv[e] = vword<DL, F32C>(blk.v[p], e);
             float pw[GM];
             for (int h = 0; h < GM; h += 4) {
-                const float4 t = *reinterpret_cast<const float4*>(&p_lds[wave][p][h]);
+                const float4 t = *reinterpret_cast<const float4*>(&p_lds[wave][p * GM + h]);
                 pw[h] = t.x;
                 pw[h + 1] = t.y;
                 pw[h + 2] = t.z;
@@ -524,6 +602,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_kernel(AttnParams a) {
             }
             for (int h = 0; h < GM; ++h)
                 for (int e = 0; e < DL; ++e) acc[h][e] += pw[h] * vv[e];
+        }
         }
         // p_lds is rewritten by this wave's next block
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -559,9 +638,19 @@ __global__ void __launch_bounds__(kAttnThreads) attn_kernel(AttnParams a) {
             st_l[wave][h] = ls;
         }
     }
-    for (int h = 0; h < GM; ++h)
-        if (h < G)
-            for (int e = 0; e < DL; ++e) st_acc[wave][h][DL * lane + e] = acc[h][e];
+    if constexpr (MV) {
+        for (int r = 0; r < 4; ++r) {
+            const int h = 4 * grp + r;
+            if (h < G)
+                for (int c = 0; c < NT; c += 4)
+                    *reinterpret_cast<float4*>(&st_acc[wave][h][NT * col + c]) =
+                        make_float4(accm[c][r], accm[c + 1][r], accm[c + 2][r], accm[c + 3][r]);
+        }
+    } else {
+        for (int h = 0; h < GM; ++h)
+            if (h < G)
+                for (int e = 0; e < DL; ++e) st_acc[wave][h][DL * lane + e] = acc[h][e];
+    }
     __syncthreads();
 
     // Merge the waves in a fixed order; write the output or the partial.
