@@ -245,6 +245,9 @@ def test_tile_graph_survives_workspace_growth():
     stays alive."""
     from breeze_amd import gemv as gemv_mod
 
+    dev = torch.cuda.current_device()
+    if dev in gemv_mod._GEMV_WS:  # start from a fresh (small) workspace, whatever ran before
+        gemv_mod._GEMV_WS_RETIRED.append(gemv_mod._GEMV_WS.pop(dev))
     c = Int4Case(O.synth(200, 1280, 1, seed=26)[0], 128)
     x = bf16_tensor(O.synth(8, 1280, 16, seed=27)[2])
     out = torch.empty(16, 200, device="cuda", dtype=torch.bfloat16)
@@ -261,14 +264,16 @@ def test_tile_graph_survives_workspace_growth():
     with torch.cuda.stream(s), torch.cuda.graph(g, stream=s):
         run()
     torch.cuda.current_stream().wait_stream(s)
-    before = gemv_mod._GEMV_WS[torch.cuda.current_device()].data_ptr()
-    # a much larger split-K call grows the workspace
+    before = gemv_mod._GEMV_WS[dev]
+    # a split-K call needing more than the fresh 1 MiB workspace grows it
     big = Int4Case(O.synth(2048, 2560, 1, seed=28)[0], 128)
-    xb = bf16_tensor(O.synth(8, 2560, 32, seed=29)[2])
-    need = G.gemv(xb, big.d_packed, G.W_INT4_ZP, 2048, sc0=big.d_sz, group=128, cfg=(0, 0, 0, PATH, 20))
+    xb_bits = O.synth(8, 2560, 32, seed=29)[2]
+    assert 20 * 32 * 2048 * 4 > before.numel() * 4
+    got = G.gemv(bf16_tensor(xb_bits), big.d_packed, G.W_INT4_ZP, 2048, sc0=big.d_sz, group=128,
+                 cfg=(0, 0, 0, PATH, 20))
     torch.cuda.synchronize()
-    assert gemv_mod._GEMV_WS[torch.cuda.current_device()].data_ptr() != before
-    _check(need, O.synth(8, 2560, 32, seed=29)[2], big.w_zp)
+    assert gemv_mod._GEMV_WS[dev].data_ptr() != before.data_ptr()
+    _check(got, xb_bits, big.w_zp)
     for i in range(3):
         out.zero_()
         g.replay()
