@@ -125,7 +125,9 @@ def test_int4_linear_buffers_and_forward(device):
     sz = O.scales_zeros(s, z)
     assert np.array_equal(bf16_bits(mod.scales_zeros), sz)
     w_eff = O.dequant_int4_zp(q, sz, 128)
-    for shape, dtype in (((1, K), torch.bfloat16), ((2, 3, K), torch.bfloat16), ((5, K), torch.float32)):
+    # M = 1..4 on the row-sliced paths; 5, 12 and 40 (two launches of <= 32 rows) on the tile kernel
+    for shape, dtype in (((1, K), torch.bfloat16), ((2, 3, K), torch.bfloat16), ((5, K), torch.float32),
+                         ((2, 6, K), torch.bfloat16), ((40, K), torch.bfloat16)):
         x = torch.randn(*shape, generator=torch.Generator().manual_seed(3)).to(dtype)
         y = mod(x.to(_dev()))
         assert y.dtype == dtype and tuple(y.shape) == shape[:-1] + (N,)
@@ -158,11 +160,12 @@ def test_fp8_linear_buffers_and_forward():
     codes, scale = O.quantize_fp8_linear(w)
     assert np.array_equal(mod.weight_fp8.view(torch.uint8).cpu().numpy(), codes)
     assert np.array_equal(mod.weight_scale.cpu().numpy()[0], scale)
-    x = torch.randn(3, K, device=_dev()).to(torch.bfloat16)
-    y = mod(x)
-    assert y.dtype == torch.bfloat16 and tuple(y.shape) == (3, N)
-    ref = O.gemv_ref(x.float().cpu().numpy(), O.dequant_fp8(codes, scale))
-    assert O.rel_err(f32(y), ref) <= TOL
+    for M in (3, 12, 40):  # row-sliced path, tile kernel, tile kernel in two launches
+        x = torch.randn(M, K, device=_dev()).to(torch.bfloat16)
+        y = mod(x)
+        assert y.dtype == torch.bfloat16 and tuple(y.shape) == (M, N)
+        ref = O.gemv_ref(x.float().cpu().numpy(), O.dequant_fp8(codes, scale))
+        assert O.rel_err(f32(y), ref) <= TOL, M
 
 
 class _Mlp(nn.Module):

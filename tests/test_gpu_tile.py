@@ -279,3 +279,26 @@ def test_tile_graph_survives_workspace_growth():
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), i
+
+
+@pytest.mark.parametrize("fmt", ["int4", "fp8"])
+def test_tile_fp32_residual_aliasing_out(fmt):
+    """Residual epilogue with an fp32 residual that is also the output
+    (in-place residual add, which the C ABI allows), several slices."""
+    N, K = SMALL[fmt]
+    M = 10
+    _, w_eff, rs = _case(fmt, N, K, seed=32)
+    x = O.synth(8, K, M, seed=33)[2]
+    res = np.random.default_rng(34).standard_normal((M, N)).astype(np.float32)
+    buf = torch.from_numpy(res.copy()).cuda()
+    w, _, _ = O.synth(N, K, 1, seed=32)
+    if fmt == "int4":
+        c = Int4Case(w, 128)
+        G.gemv(bf16_tensor(x), c.d_packed, G.W_INT4_ZP, N, sc0=c.d_sz, group=128, epilogue=G.EPI_RESIDUAL,
+               residual=buf, out=buf, cfg=(0, 0, 0, PATH, 4))
+    else:
+        c = Fp8Case(w)
+        G.gemv(bf16_tensor(x), c.d_codes, G.W_FP8, N, sc0=c.d_scale, epilogue=G.EPI_RESIDUAL, residual=buf,
+               out=buf, cfg=(0, 0, 0, PATH, 4))
+    ref = O.gemv_ref(O.bf16_bits_to_f32(x), w_eff, O.EPI_RES, res, rs)
+    assert O.rel_err(f32(buf), ref) <= TIGHT
