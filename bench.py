@@ -18,9 +18,10 @@ call's algorithmic bytes are packed weights + scales + x + gamma + output
                committed summary holds them;
   cpu_baseline the same MLP step as dequantize-then-matmul in torch on the
                host cores (a bounded sample of steps);
-  detail       per-kernel times and the full synthetic decode step
-               (26 int4 decoder layers + bf16 head) in µs against its
-               bytes-moved roofline.
+  detail       per-kernel times, the full synthetic decode step (26 int4
+               decoder layers + bf16 head) in µs against its bytes-moved
+               roofline, the C1-C4 GEMV table, the fused attention step and
+               the fp32 heads, each against its HBM roofline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-step]
 
@@ -266,6 +267,8 @@ def main() -> int:
         detail["decode_step_attn"] = decode_step(torch, G, dev, log, 2, attn_pos=1023, cache_len=1024)
     if not args.no_configs:
         detail["configs"] = config_table(torch, G, dev, log)
+        detail["attention"] = attention_table(torch, dev, log)
+        detail["fp32_heads"] = heads_table(torch, dev, log)
 
     # ---- CPU baseline: same MLP step on the host cores (bounded sample)
     cpu = None
@@ -503,6 +506,101 @@ def config_table(torch, G, dev, log) -> list:
             log(f"{name:42s} M={M:2d}: {us:7.2f} us  {nbytes / us / 1e3:6.0f} GB/s  "
                 f"({roof / us * 100:4.1f}% of roofline)")
         del copies
+        torch.cuda.empty_cache()
+    return rows
+
+
+def attention_table(torch, dev, log) -> list:
+    """The fused decode-attention step alone (q/k RMSNorm + RoPE + cache
+    write + attention over cache positions [0, pos] + split combine) of the
+    C5 geometry: 16 query heads and 4 KV heads of 256, bf16 caches of 1024 /
+    2048 positions, M = 1 and 2, the library's default split.  Timed as HIP-
+    graph replays over caches rotating through >= 1 GiB, so the keys and
+    values stream from HBM.  Roofline bytes: keys and values over [0, pos]
+    read once, the token's qkv row, norm weights, cos/sin, the new key and
+    value written, the mask row and the output."""
+    from breeze_amd import attention as AT
+    from breeze_amd.fused.kernels import graph_time_us
+
+    HQ, HKV, D = 16, 4, 256
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    rows = []
+    for S in (1024, 2048):
+        for M in (1, 2):
+            per = 2 * 2 * M * HKV * S * D  # one cache pair
+            ncopy = max(2, -(-(1 << 30) // per))
+            caches = [(torch.randn(M, HKV, S, D, device=dev, generator=gen).to(torch.bfloat16),
+                       torch.randn(M, HKV, S, D, device=dev, generator=gen).to(torch.bfloat16)) for _ in range(ncopy)]
+            qkv = torch.randn(M, (HQ + 2 * HKV) * D, device=dev, generator=gen).to(torch.bfloat16)
+            th = torch.rand(M, D // 2, device=dev, generator=gen) * 6
+            cos = torch.cat([th.cos(), th.cos()], -1).to(torch.bfloat16)
+            sin = torch.cat([th.sin(), th.sin()], -1).to(torch.bfloat16)
+            qn = (1 + 0.1 * torch.randn(D, device=dev, generator=gen)).to(torch.bfloat16)
+            kn = (1 + 0.1 * torch.randn(D, device=dev, generator=gen)).to(torch.bfloat16)
+            mask = torch.zeros(M, 1, 1, S, device=dev, dtype=torch.bfloat16)
+            out = torch.empty(M, HQ * D, device=dev, dtype=torch.bfloat16)
+            split = AT.default_split(S)
+            for p in (127, S - 1):
+                pos = torch.tensor([p], device=dev)
+                st = {"i": 0}
+
+                def fn():
+                    k, v = caches[st["i"] % ncopy]
+                    st["i"] += 1
+                    AT.attention_step(qkv, cos, sin, pos, k, v, mask, qn, kn, EPS, out, split=split)
+
+                us = graph_time_us(fn, iters=min(2 * ncopy, 128))
+                nbytes = (2 * 2 * M * HKV * (p + 1) * D + 2 * M * (HQ + 2 * HKV) * D + 2 * 2 * D + 2 * 2 * M * D
+                          + 2 * 2 * M * HKV * D + 2 * M * S + 2 * M * HQ * D)
+                roof = nbytes / HBM_PEAK_GBPS / 1e3
+                rows.append({"cache": S, "M": M, "pos": p, "split": split, "us": round(us, 2),
+                             "gbps": round(nbytes / us / 1e3, 1), "roofline_us": round(roof, 3),
+                             "frac": round(roof / us, 3)})
+                log(f"attention step S={S} M={M} pos={p:4d} split={split}: {us:6.2f} us "
+                    f"({nbytes / us / 1e3:5.0f} GB/s, {roof / us * 100:4.1f}% of roofline)")
+            del caches
+            torch.cuda.empty_cache()
+    return rows
+
+
+def heads_table(torch, dev, log) -> list:
+    """The fp32 heads the reference keeps unquantized: the backbone lm_head
+    2052 x 2048 at M = 1, 2 (CFG) and one depth codebook head 2051 x 1024
+    (picked from 15 by a device index), each as fp32 weights rotating through
+    >= 1 GiB.  Roofline bytes: the fp32 weight matrix + x + output."""
+    from breeze_amd.fused.kernels import graph_time_us
+    from breeze_amd.heads import head_f32
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    rows = []
+    for name, N, K, C, Ms in (("backbone lm_head", 2052, 2048, 1, (1, 2)), ("depth codebook head", 2051, 1024, 15, (1,))):
+        w = (torch.randn(C, N, K, device=dev, generator=gen) * 0.02) if C > 1 else \
+            (torch.randn(N, K, device=dev, generator=gen) * 0.02)
+        per = w.numel() * 4
+        ncopy = max(2, -(-(1 << 30) // per))
+        ws = [w.clone() for _ in range(ncopy)]
+        index = torch.tensor([7], device=dev, dtype=torch.int64)
+        for M in Ms:
+            x = torch.randn(M, K, device=dev, generator=gen)
+            out = torch.empty(M, N, device=dev)
+            st = {"i": 0}
+
+            def fn():
+                wi = ws[st["i"] % ncopy]
+                st["i"] += 1
+                head_f32(x, wi, index=index if C > 1 else None, out=out)
+
+            us = graph_time_us(fn, iters=min(2 * ncopy, 128))
+            nbytes = 4 * N * K + 4 * M * K + 4 * M * N
+            roof = nbytes / HBM_PEAK_GBPS / 1e3
+            rows.append({"head": f"{name} {N}x{K} fp32" + (f" (1 of {C}, device index)" if C > 1 else ""),
+                         "M": M, "us": round(us, 2), "gbps": round(nbytes / us / 1e3, 1),
+                         "roofline_us": round(roof, 3), "frac": round(roof / us, 3)})
+            log(f"fp32 head {name} {N}x{K} M={M}: {us:6.2f} us ({nbytes / us / 1e3:5.0f} GB/s, "
+                f"{roof / us * 100:4.1f}% of roofline)")
+        del ws, w
         torch.cuda.empty_cache()
     return rows
 

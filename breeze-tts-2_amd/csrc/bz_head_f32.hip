@@ -11,10 +11,13 @@
 // host round trip and can sit in a captured graph.  A selection outside
 // [0, nmat) writes zeros.
 //
-// Layout of the work: x rows (up to kHeadMaxRows per launch) in LDS as fp32;
-// each wave owns kHeadRowsPerWave output rows n and streams them with
-// 16-byte loads (64 lanes cover 256 k per load), fp32 products summed per
-// lane, then across the wave (DPP row sums, rows 0..3 in order).
+// Layout of the work: x rows (up to kHeadMaxRows per launch) in LDS as fp32,
+// loaded into registers before the first weights are requested (vector loads
+// retire in order, so staging x then waits for x alone); each wave owns
+// kHeadRowsPerWave output rows n and streams them with 16-byte loads (64
+// lanes cover 256 k per load), up to 8 such loads per row issued together
+// so a 2048-k row takes one memory round trip; fp32 products are summed per
+// lane in k order, then across the wave (DPP row sums, rows 0..3 in order).
 #include "bz_device.h"
 #include "bz_gemv.h"
 
@@ -37,7 +40,10 @@ __device__ __forceinline__ float head_row_sum(float v) {
            __int_as_float(__builtin_amdgcn_readlane(b, 48));
 }
 
-template <int M>
+// S = 256-k loads per row issued together (min(8, K / 256), so no load is
+// issued past a row for K a multiple of 256 S; the last chunk of other K
+// clamps its indices into the row).
+template <int M, int S>
 __global__ void __launch_bounds__(kHeadThreads) head_f32_kernel(const float* x, int64_t ldx, int K, const float* w,
                                                                int64_t mat_stride, int nmat, const int64_t* index,
                                                                int64_t index_offset, int N, float* out, int64_t ldo) {
@@ -45,28 +51,64 @@ __global__ void __launch_bounds__(kHeadThreads) head_f32_kernel(const float* x, 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t sel = (index ? *index : 0) + index_offset;
-    for (int i = tid * 4; i < M * K; i += kHeadThreads * 4) {
-        const int m = i / K, k = i - m * K;  // K % 4 == 0: a float4 never crosses rows
-        *reinterpret_cast<float4*>(xs + i) = *reinterpret_cast<const float4*>(x + m * ldx + k);
-    }
-    __syncthreads();
-    const int n0 = (blockIdx.x * kHeadWaves + wave) * kHeadRowsPerWave;
-    if (n0 >= N) return;
     const bool ok = sel >= 0 && sel < nmat;
     const float* wm = w + (ok ? sel : 0) * mat_stride;
+    const int n0 = (blockIdx.x * kHeadWaves + wave) * kHeadRowsPerWave;  // rows past N load row N - 1
+
+    // 1. x into registers first (float4 e = tid + 256 i: row 4e / K), so
+    //    waiting for it does not wait for the weights issued after it
+    constexpr int XV = M * kHeadMaxK / (4 * kHeadThreads);
+    const int nx = M * (K >> 2);
+    float4 xr[XV];
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+        const int e = min(tid + i * kHeadThreads, nx - 1);
+        const int m = (4 * e) / K;
+        xr[i] = *reinterpret_cast<const float4*>(x + m * ldx + (4 * e - m * K));
+    }
+    // 2. the first chunk of weights (S loads of 256 k per row)
+    const float* wrow[kHeadRowsPerWave];
+    for (int r = 0; r < kHeadRowsPerWave; ++r) wrow[r] = wm + (int64_t)min(n0 + r, N - 1) * K;
+    float4 wv[S][kHeadRowsPerWave];
+    auto load_chunk = [&](int k0) {
+#pragma unroll
+        for (int u = 0; u < S; ++u) {
+            const int k = min(k0 + 256 * u + 4 * lane, K - 4);
+#pragma unroll
+            for (int r = 0; r < kHeadRowsPerWave; ++r) wv[u][r] = *reinterpret_cast<const float4*>(wrow[r] + k);
+        }
+    };
+    load_chunk(0);  // (no scheduling barrier here: one made the compiler spill xr)
+    // 3. stage x (clamped entries hold element nx - 1 and store it again:
+    //    unconditional stores keep xr in registers)
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+        const int e = min(tid + i * kHeadThreads, nx - 1);
+        *reinterpret_cast<float4*>(xs + 4 * e) = xr[i];
+    }
+    __syncthreads();
+    if (n0 >= N) return;
+
     float acc[kHeadRowsPerWave][M];
     for (int r = 0; r < kHeadRowsPerWave; ++r)
         for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
-    for (int k = 4 * lane; k < K; k += 256) {
-        float4 wv[kHeadRowsPerWave];
-        for (int r = 0; r < kHeadRowsPerWave; ++r) {
-            const int n = min(n0 + r, N - 1);
-            wv[r] = *reinterpret_cast<const float4*>(wm + (int64_t)n * K + k);
+    for (int k0 = 0; k0 < K; k0 += 256 * S) {
+#pragma unroll
+        for (int u = 0; u < S; ++u) {
+            const int k = k0 + 256 * u + 4 * lane;
+            if (k < K) {  // lane-uniform except in a row's last chunk
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const float4 xv = *reinterpret_cast<const float4*>(xs + m * K + k);
+#pragma unroll
+                    for (int r = 0; r < kHeadRowsPerWave; ++r)
+                        acc[r][m] += wv[u][r].x * xv.x + wv[u][r].y * xv.y + wv[u][r].z * xv.z + wv[u][r].w * xv.w;
+                }
+            }
         }
-        for (int m = 0; m < M; ++m) {
-            const float4 xv = *reinterpret_cast<const float4*>(xs + m * K + k);
-            for (int r = 0; r < kHeadRowsPerWave; ++r)
-                acc[r][m] += wv[r].x * xv.x + wv[r].y * xv.y + wv[r].z * xv.z + wv[r].w * xv.w;
+        if (k0 + 256 * S < K) {
+            load_chunk(k0 + 256 * S);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     for (int r = 0; r < kHeadRowsPerWave; ++r) {
@@ -74,6 +116,29 @@ __global__ void __launch_bounds__(kHeadThreads) head_f32_kernel(const float* x, 
             const float s = head_row_sum(acc[r][m]);
             if (lane == 0 && n0 + r < N) out[m * ldo + n0 + r] = ok ? s : 0.0f;
         }
+    }
+}
+
+template <int M>
+static void launch_head_m(int steps, dim3 grid, size_t lds, hipStream_t st, const float* x, int64_t ldx, int K,
+                          const float* w, int64_t mat_stride, int nmat, const int64_t* index, int64_t index_offset,
+                          int N, float* out, int64_t ldo) {
+    switch (steps) {
+        case 8: hipLaunchKernelGGL((head_f32_kernel<M, 8>), grid, dim3(kHeadThreads), lds, st, x, ldx, K, w, mat_stride, nmat, index, index_offset, N, out, ldo); break;
+        case 4: hipLaunchKernelGGL((head_f32_kernel<M, 4>), grid, dim3(kHeadThreads), lds, st, x, ldx, K, w, mat_stride, nmat, index, index_offset, N, out, ldo); break;
+        case 2: hipLaunchKernelGGL((head_f32_kernel<M, 2>), grid, dim3(kHeadThreads), lds, st, x, ldx, K, w, mat_stride, nmat, index, index_offset, N, out, ldo); break;
+        default: hipLaunchKernelGGL((head_f32_kernel<M, 1>), grid, dim3(kHeadThreads), lds, st, x, ldx, K, w, mat_stride, nmat, index, index_offset, N, out, ldo); break;
+    }
+}
+
+static void launch_head(int rows, int steps, dim3 grid, size_t lds, hipStream_t st, const float* x, int64_t ldx,
+                        int K, const float* w, int64_t mat_stride, int nmat, const int64_t* index,
+                        int64_t index_offset, int N, float* out, int64_t ldo) {
+    switch (rows) {
+        case 1: launch_head_m<1>(steps, grid, lds, st, x, ldx, K, w, mat_stride, nmat, index, index_offset, N, out, ldo); break;
+        case 2: launch_head_m<2>(steps, grid, lds, st, x, ldx, K, w, mat_stride, nmat, index, index_offset, N, out, ldo); break;
+        case 3: launch_head_m<3>(steps, grid, lds, st, x, ldx, K, w, mat_stride, nmat, index, index_offset, N, out, ldo); break;
+        default: launch_head_m<4>(steps, grid, lds, st, x, ldx, K, w, mat_stride, nmat, index, index_offset, N, out, ldo); break;
     }
 }
 
@@ -98,12 +163,8 @@ extern "C" int bz_head_f32(const float* x, int64_t ldx, int32_t M, int32_t K, co
         const float* xm = x + (int64_t)m0 * ldx;
         float* om = out + (int64_t)m0 * ldo;
         const size_t lds = (size_t)rows * K * sizeof(float);
-        switch (rows) {
-            case 1: hipLaunchKernelGGL(head_f32_kernel<1>, grid, dim3(kHeadThreads), lds, st, xm, ldx, K, w, mat_stride, nmat, index, index_offset, N, om, ldo); break;
-            case 2: hipLaunchKernelGGL(head_f32_kernel<2>, grid, dim3(kHeadThreads), lds, st, xm, ldx, K, w, mat_stride, nmat, index, index_offset, N, om, ldo); break;
-            case 3: hipLaunchKernelGGL(head_f32_kernel<3>, grid, dim3(kHeadThreads), lds, st, xm, ldx, K, w, mat_stride, nmat, index, index_offset, N, om, ldo); break;
-            default: hipLaunchKernelGGL(head_f32_kernel<4>, grid, dim3(kHeadThreads), lds, st, xm, ldx, K, w, mat_stride, nmat, index, index_offset, N, om, ldo); break;
-        }
+        const int steps = K >= 2048 ? 8 : (K >= 1024 ? 4 : (K >= 512 ? 2 : 1));
+        launch_head(rows, steps, grid, lds, st, xm, ldx, K, w, mat_stride, nmat, index, index_offset, N, om, ldo);
         if (hipGetLastError() != hipSuccess) return BZ_ERR_LAUNCH;
     }
     return BZ_OK;
