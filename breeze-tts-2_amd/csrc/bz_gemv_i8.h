@@ -239,6 +239,20 @@ __global__ void __launch_bounds__(kMaxThreads) gemv_i8mma(GemvParams p, int M) {
     //    flight
     i8_finish_x(p, M, xr, gr, x8, xsx, tid, nthr);
     __syncthreads();
+    // 1/rms per row from the units' sums of x^2, in unit order, while the
+    // first weights are in flight (read after the epilogue's barrier)
+    if (tid < M) {
+        float inv = 1.0f;
+        if (p.norm) {
+            const int units = p.K >> 7;
+            const float* sq = xsx + tid * units * 4 + 2;
+            float ss = 0.0f;
+            for (int u0 = 0; u0 < units; u0 += 8)  // 8 reads in flight, one running sum in unit order
+                ss = sum_strided<8>(sq + u0 * 4, 4, min(8, units - u0), ss);
+            inv = rsqrtf(ss / (float)p.K + p.eps);
+        }
+        invs[tid] = inv;
+    }
 
     // 2. every unit once
     f32x4_t acc[T];
@@ -258,16 +272,6 @@ __global__ void __launch_bounds__(kMaxThreads) gemv_i8mma(GemvParams p, int M) {
             }
         }
     });
-    if (tid < M) {  // 1/rms per row from the units' sums of x^2, in unit order
-        float inv = 1.0f;
-        if (p.norm) {
-            const int units = p.K >> 7;
-            float ss = 0.0f;
-            for (int u = 0; u < units; ++u) ss += xsx[(tid * units + u) * 4 + 2];
-            inv = rsqrtf(ss / (float)p.K + p.eps);
-        }
-        invs[tid] = inv;
-    }
     __syncthreads();
 
     // 3. epilogue (runtime M): fixed-order sum of the waves' partials, 1/rms,
@@ -281,8 +285,7 @@ __global__ void __launch_bounds__(kMaxThreads) gemv_i8mma(GemvParams p, int M) {
         float a[T];
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            float v = 0.0f;
-            for (int w = 0; w < NW; ++w) v += red[(((tl * NW + w) * T + t) * M + m) * 16 + q];
+            const float v = sum_strided<kMaxWaves>(red + ((tl * NW * T + t) * M + m) * 16 + q, T * M * 16, NW);
             a[t] = v * inv;
         }
         float o = SILU ? silu(a[0]) * a[T - 1] : a[0];

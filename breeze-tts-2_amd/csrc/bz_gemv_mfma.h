@@ -230,6 +230,8 @@ __global__ void __launch_bounds__(kMaxThreads) gemv_mfma(GemvParams p) {
     // 1. staging completes while the weights are in flight
     finish_x_mfma<WF, M>(p, xr, gr, xs, x128, nrm, tid, nthr, wave, lane);
     __syncthreads();
+    float inv[M];
+    row_inv_all<M>(p, nrm, NW, inv);
 
     // 2. every unit once; a wave's partial sums of a tile go to LDS after its
     //    last unit in that tile
@@ -254,7 +256,7 @@ __global__ void __launch_bounds__(kMaxThreads) gemv_mfma(GemvParams p) {
     __syncthreads();
 
     // 3. epilogue
-    epilogue<WF, M, T, SILU, 16>(p, tile0, ntl, tid, nthr, NW, red, nrm, pre);
+    epilogue<WF, M, T, SILU, 16>(p, tile0, ntl, tid, nthr, NW, red, inv, pre);
 }
 
 template <int WF, int M, int T, int D, bool SILU>
