@@ -44,6 +44,7 @@ import argparse
 import json
 import os
 import re
+import statistics
 import sys
 import time
 
@@ -230,18 +231,21 @@ def main() -> int:
     del gk
     value_tbps = step_bytes * args.steps / (ms * 1e-3) / 1e12
 
-    # ---- dominant kernel alone: gate|up, back-to-back launches on one stream
+    # ---- dominant kernel alone: gate|up, back-to-back launches on one stream;
+    #      the median of three replays (one replay disturbed by, e.g., a
+    #      profiler's buffer flush does not move it)
     reps = 4 * ncopy
+
+    def per_launch_us(g):
+        timed(g)
+        return statistics.median(timed(g)[0] for _ in range(3)) * 1e3 / reps
+
     g_gu = capture(lambda i: gate_up(copies[i % ncopy]), reps)
-    timed(g_gu)
-    ms_gu, _ = timed(g_gu)
+    us_gu = per_launch_us(g_gu)
     del g_gu
-    us_gu = ms_gu * 1e3 / reps
     g_dn = capture(lambda i: down(copies[i % ncopy]), reps)
-    timed(g_dn)
-    ms_dn, _ = timed(g_dn)
+    us_dn = per_launch_us(g_dn)
     del g_dn
-    us_dn = ms_dn * 1e3 / reps
     achieved = b_gu / (us_gu * 1e-6) / 1e9
     traffic = read_traffic()
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
