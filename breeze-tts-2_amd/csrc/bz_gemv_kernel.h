@@ -274,13 +274,18 @@ __device__ __forceinline__ float row_inv_rms(const GemvParams& p, const float* n
     return rsqrtf(s / (float)p.K + p.eps);
 }
 
-// Every row's 1/rms, computed right after the x-staging barrier: its LDS
-// reads, divide and rsqrt then run while the first weight loads are in
-// flight instead of lengthening the epilogue.
+// For M <= 2 every row's 1/rms is computed right after the x-staging
+// barrier: its LDS reads, divide and rsqrt then run while the first weight
+// loads are in flight instead of lengthening the epilogue.  For more rows
+// the epilogue computes it: a register array kept across the main loop and
+// selected by the output's row is turned into a scratch array.
+template <int M>
+constexpr bool kEarlyInv = M <= 2;
+
 template <int M>
 __device__ __forceinline__ void row_inv_all(const GemvParams& p, const float* nrm, int NW, float (&inv)[M]) {
 #pragma unroll
-    for (int m = 0; m < M; ++m) inv[m] = row_inv_rms(p, nrm, NW, M, m);
+    for (int m = 0; m < M; ++m) inv[m] = kEarlyInv<M> ? row_inv_rms(p, nrm, NW, M, m) : 1.0f;
 }
 
 // ---------------------------------------------------------------------------
@@ -332,7 +337,11 @@ __device__ __forceinline__ EpiPrefetch<T> epi_prefetch(const GemvParams& p, int 
 // and store.  red[((tl*NW + w)*T + t)*M + m][COLS].
 template <int WF, int M, int T, bool SILU, int COLS>
 __device__ __forceinline__ void epilogue(const GemvParams& p, int tile0, int ntl, int tid, int nthr, int NW,
-                                         const float* red, const float (&inv)[M], const EpiPrefetch<T>& pre) {
+                                         const float* red, const float* nrm, const float (&early)[M],
+                                         const EpiPrefetch<T>& pre) {
+    float inv[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) inv[m] = kEarlyInv<M> ? early[m] : row_inv_rms(p, nrm, NW, M, m);
     for (int i = tid; i < ntl * M * COLS; i += nthr) {
         const OutIndex<M, COLS> o(i, tile0);
         if (o.c >= p.n_out) continue;
@@ -650,7 +659,7 @@ __global__ void __launch_bounds__(kMaxThreads) gemv_persist(GemvParams p) {
     __syncthreads();
 
     // 3. epilogue
-    epilogue<WF, M, T, SILU, 8>(p, tile0, ntl, tid, nthr, NW, red, inv, pre);
+    epilogue<WF, M, T, SILU, 8>(p, tile0, ntl, tid, nthr, NW, red, nrm, inv, pre);
 }
 
 // ---------------------------------------------------------------------------

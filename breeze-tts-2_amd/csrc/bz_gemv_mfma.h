@@ -256,7 +256,7 @@ __global__ void __launch_bounds__(kMaxThreads) gemv_mfma(GemvParams p) {
     __syncthreads();
 
     // 3. epilogue
-    epilogue<WF, M, T, SILU, 16>(p, tile0, ntl, tid, nthr, NW, red, inv, pre);
+    epilogue<WF, M, T, SILU, 16>(p, tile0, ntl, tid, nthr, NW, red, nrm, inv, pre);
 }
 
 template <int WF, int M, int T, int D, bool SILU>
