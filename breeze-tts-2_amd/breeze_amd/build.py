@@ -10,6 +10,7 @@ parallel) and linked with hipcc.
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -38,6 +39,34 @@ HIP_FLAGS = [
 ]
 
 
+# Kernels of the decode paths that must not use scratch (private memory): a
+# spilled or dynamically indexed register array costs a memory round trip per
+# access.  Patterns over the mangled names; the attention kernel's bf16-cache
+# instances with D <= 256 (attn_kernel<DL = 1, 2, 4, GM, F32C = false, ...>)
+# are covered, its fp32-cache and D = 512 instances are allowed scratch.
+NO_SCRATCH = (r"gemv_persist", r"gemv_mfma", r"gemv_i8mma", r"gemv_tile", r"head_f32", r"qkv_rope_cache",
+              r"attn_kernelILi[124]ELi\d+ELb0E")
+
+
+def kernel_resources(remarks: str) -> list[tuple[str, int, int]]:
+    """(kernel, VGPRs, scratch bytes per lane) from hipcc's
+    -Rpass-analysis=kernel-resource-usage remarks."""
+    out, name, vgpr = [], None, 0
+    for line in remarks.splitlines():
+        if "remark:" not in line:
+            continue
+        body = line.split("remark:", 1)[1].strip()
+        body = body.split(" [-Rpass", 1)[0]
+        if body.startswith("Function Name:"):
+            name, vgpr = body.split(":", 1)[1].strip(), 0
+        elif body.startswith("VGPRs:") and name:
+            vgpr = int(body.split(":")[1].split()[0])
+        elif body.startswith("ScratchSize") and name:
+            out.append((name, vgpr, int(body.split(":")[1].split()[0])))
+            name = None
+    return out
+
+
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -59,18 +88,25 @@ def build(verbose: bool = False) -> Path:
     if not srcs:
         raise RuntimeError(f"no HIP sources under {SRC_DIR}")
 
-    def compile_one(src: Path) -> Path:
+    def compile_one(src: Path) -> tuple[Path, list]:
         obj = obj_dir / (src.stem + ".o")
-        cmd = [hipcc, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+        cmd = [hipcc, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}\n{res.stderr}")
-        return obj
+        return obj, kernel_resources(res.stderr)
 
     with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as pool:
-        objs = list(pool.map(compile_one, srcs))
+        done = list(pool.map(compile_one, srcs))
+    objs = [o for o, _ in done]
+    kernels = sorted({k for _, ks in done for k in ks})
+    (obj_dir / "kernel_resources.txt").write_text(
+        "".join(f"{vg:4d} vgpr {sc:6d} scratch  {name}\n" for name, vg, sc in kernels))
+    spilled = [name for name, _, sc in kernels if sc and any(re.search(t, name) for t in NO_SCRATCH)]
+    if spilled:
+        raise RuntimeError("decode kernels using scratch memory:\n  " + "\n  ".join(spilled))
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     if verbose:
