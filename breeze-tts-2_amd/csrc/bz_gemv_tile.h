@@ -113,6 +113,52 @@ __device__ __forceinline__ void tile_store(const GemvParams& p, float v, int r, 
         reinterpret_cast<uint16_t*>(p.out)[oi] = f32_to_bf16(v);
 }
 
+// The last arrival's sum of a column block's partials over the slices, in
+// slice order, and the epilogue: each thread sums RQ outputs per pass, RS
+// slices of each in flight per batch (indices clamped into range, so the
+// loads stay straight-line).
+template <int WF, int RQ, int RS>
+__device__ __forceinline__ void tile_sum_slices(const TileParams& tp, int cb, int CBW, int nout, int64_t sstride,
+                                                int tid, int nthr) {
+    const GemvParams& p = tp.p;
+    const int nsl = tp.nsl;
+    const int cbw_log2 = __builtin_ctz(CBW);
+    for (int i0 = 0; i0 < nout; i0 += RQ * nthr) {
+        float sum[RQ];
+        int off[RQ];
+#pragma unroll
+        for (int q = 0; q < RQ; ++q) {
+            sum[q] = 0.0f;
+            const int i = min(i0 + tid + q * nthr, nout - 1);
+            const int r = i >> cbw_log2;
+            off[q] = r * p.n_out + min(cb * CBW + (i - r * CBW), p.n_out - 1);
+        }
+        for (int s0 = 0; s0 < nsl; s0 += RS) {
+            float v[RQ][RS];
+#pragma unroll
+            for (int u = 0; u < RS; ++u) {
+                const float* ps = tp.part + min(s0 + u, nsl - 1) * sstride;  // uniform
+#pragma unroll
+                for (int q = 0; q < RQ; ++q)
+                    v[q][u] = __hip_atomic_load(ps + off[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int q = 0; q < RQ; ++q)
+#pragma unroll
+                for (int u = 0; u < RS; ++u)
+                    if (s0 + u < nsl) sum[q] += v[q][u];
+        }
+#pragma unroll
+        for (int q = 0; q < RQ; ++q) {
+            const int i = i0 + tid + q * nthr;
+            if (i >= nout) continue;
+            const int r = i >> cbw_log2;
+            const int c = cb * CBW + (i - r * CBW);
+            if (c < p.n_out) tile_store<WF>(p, sum[q], r, c);
+        }
+    }
+}
+
 template <int WF, int MB, int T, int D>
 __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -334,44 +380,17 @@ __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
     }
     __syncthreads();
     if (!last_arrival) return;
-    // Each thread sums 4 outputs, 4 slices of each in flight per batch;
-    // slices are added in slice order.
+    // The sum over slices, in slice order.  Threads with 8 or more outputs
+    // (M = 32 of a 128-column block over 512 threads) take 8 outputs x 4
+    // slices of loads per batch, which halves the memory round trips of
+    // 4 x 4; fewer outputs keep 4 x 4, since unused (clamped) loads of the
+    // wider batch still cost requests.
     const int CBW = NW * 16 * T;  // columns of a block (a power of two)
-    const int cbw_log2 = __builtin_ctz(CBW);
     const int nout = M * CBW;
-    for (int i0 = 0; i0 < nout; i0 += 4 * nthr) {
-        float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        int off[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int i = min(i0 + tid + q * nthr, nout - 1);
-            const int r = i >> cbw_log2;
-            off[q] = r * p.n_out + min(cb * CBW + (i - r * CBW), p.n_out - 1);
-        }
-        for (int s0 = 0; s0 < nsl; s0 += 4) {
-            float v[4][4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float* ps = tp.part + min(s0 + u, nsl - 1) * sstride;  // uniform
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    v[q][u] = __hip_atomic_load(ps + off[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    if (s0 + u < nsl) sum[q] += v[q][u];
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int i = i0 + tid + q * nthr;
-            if (i >= nout) continue;
-            const int r = i >> cbw_log2;
-            const int c = cb * CBW + (i - r * CBW);
-            if (c < p.n_out) tile_store<WF>(p, sum[q], r, c);
-        }
-    }
+    if (nout >= 8 * nthr)
+        tile_sum_slices<WF, 8, 4>(tp, cb, CBW, nout, sstride, tid, nthr);
+    else
+        tile_sum_slices<WF, 4, 4>(tp, cb, CBW, nout, sstride, tid, nthr);
     if (tid == 0) __hip_atomic_store(&tp.cnt[cb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
