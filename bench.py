@@ -107,6 +107,8 @@ def main() -> int:
                     help="summarize two rocprofv3 --pmc runs of --profile-gateup")
     ap.add_argument("--profile-tiles", action="store_true",
                     help="only launch the several-row (C4, M = 16 and 32) GEMVs eagerly, for counter runs")
+    ap.add_argument("--profile-depth", action="store_true",
+                    help="only build and time the depth-decoder frame graph, for kernel-trace runs")
     ap.add_argument("--mfma-summary", nargs=2, metavar=("TRACE_DIR", "PMC_DIR"),
                     help="summarize a rocprofv3 --kernel-trace run and a --pmc run of --profile-tiles")
     args = ap.parse_args()
@@ -136,6 +138,9 @@ def main() -> int:
     log(f"device {torch.cuda.get_device_name(0)}")
     if args.profile_tiles:
         return profile_tiles(torch, G, dev)
+    if args.profile_depth:
+        print(json.dumps({"depth_frame": depth_frame(torch, dev, log)}), flush=True)
+        return 0
 
     # ---- synthetic C2 weights (seed 0: W, then gamma, then x, on the CPU)
     K1, N1, K2, N2, M = 2560, 20480, 10240, 2560, 1
@@ -269,6 +274,7 @@ def main() -> int:
         detail["decode_step"] = decode_step(torch, G, dev, log, 1)
         detail["decode_step_m2"] = decode_step(torch, G, dev, log, 2)
         detail["decode_step_attn"] = decode_step(torch, G, dev, log, 2, attn_pos=1023, cache_len=1024)
+        detail["depth_frame"] = depth_frame(torch, dev, log)
     if not args.no_configs:
         detail["configs"] = config_table(torch, G, dev, log)
         detail["attention"] = attention_table(torch, dev, log)
@@ -710,6 +716,75 @@ def decode_step(torch, G, dev, log, M: int = 1, attn_pos: int | None = None, cac
            "x_roofline": round(us / roof, 3), "M": M}
     if attn_pos is not None:
         res.update(attn_pos=attn_pos, cache_len=cache_len)
+    return res
+
+
+def depth_frame(torch, dev, log) -> dict:
+    """One depth-decoder frame at the reference's depth shape: 12 decoder
+    layers (hidden 1024, MLP 8192, 8 q / 2 kv heads of 128), 16 codebooks of
+    2051 tokens, embeddings of width 2048, fp8 layers (the service's
+    `--fp8 depth`), CFG batch 2, greedy; random weights.  The whole frame --
+    the 2-position start and 14 single-token steps through the fused layers,
+    the fp32 codebook heads and the sampling -- is one DepthDecodeGraph
+    replay.  Roofline bytes: per position every layer's fp8 weights and row
+    scales and the inputs projector (bf16) once, plus each step's fp32
+    codebook head matrix."""
+    import types
+
+    from transformers import Qwen3Config
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3Model
+
+    from breeze_amd.fused.depth_graph import DepthDecodeGraph
+    from breeze_amd.fused.install import install_fused_depth
+
+    H, I, L, HQ, HKV, D, C, V, E = 1024, 8192, 12, 8, 2, 128, 16, 2051, 2048
+    cfg = Qwen3Config(hidden_size=H, intermediate_size=I, num_attention_heads=HQ, num_key_value_heads=HKV,
+                      head_dim=D, num_hidden_layers=L, rms_norm_eps=1e-6, max_position_embeddings=64, vocab_size=V)
+    cfg._attn_implementation = "eager"
+    cfg.num_codebooks = C
+    cfg.backbone_hidden_size = E
+    torch.manual_seed(0)
+    with torch.device(dev):
+        m = Qwen3Model(cfg).to(torch.bfloat16).eval()
+        m.embed_tokens = torch.nn.Embedding(C * V, E, dtype=torch.bfloat16)
+        m.inputs_embeds_projector = torch.nn.Linear(E, H, bias=False, dtype=torch.bfloat16)
+        m.backbone_hidden_state_projector = None
+        with torch.no_grad():
+            for prm in m.parameters():
+                if prm.dim() == 2:
+                    prm.normal_(0, 0.02)
+        head = types.SimpleNamespace(weight=torch.randn(C - 1, H, V) * 0.02, num_codebooks=C)
+    install_fused_depth(types.SimpleNamespace(depth_decoder=types.SimpleNamespace(model=m)), batch_size=2,
+                        mlp_bits=8, attn_bits=8)
+    g = DepthDecodeGraph(types.SimpleNamespace(model=m, codebooks_head=head), batch_size=2, do_sample=False,
+                         guidance_scale=3.0)
+    bh = torch.randn(2, E, device=dev).to(torch.bfloat16)
+    first = torch.tensor([5, 5], device=dev)
+    g.run(bh, first)  # stages the inputs; the eager frame also warms the allocator
+    g.capture(num_warmup=2)
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    reps = 20
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_ev.record()
+    for _ in range(reps):
+        g.replay()
+    e_ev.record()
+    torch.cuda.synchronize()
+    us = s_ev.elapsed_time(e_ev) * 1e3 / reps
+    qkv = (HQ + 2 * HKV) * D
+    layer = (H * qkv + HQ * D * H + 2 * I * H + I * H) + 4 * (qkv + H + 2 * I + H)
+    positions = 2 + (C - 2)
+    nbytes = positions * (L * layer + 2 * E * H) + (C - 1) * V * H * 4
+    roof = nbytes / HBM_PEAK_GBPS / 1e3
+    log(f"depth frame (12 fp8 layers, 16 positions, 15 fp32 codebook heads, CFG 2, greedy): {us:.1f} us, "
+        f"roofline {roof:.1f} us ({us / roof:.1f}x)")
+    res = {"us": round(us, 1), "algorithmic_bytes": nbytes, "roofline_us": round(roof, 2),
+           "x_roofline": round(us / roof, 2), "positions": positions, "layers": L, "batch": 2,
+           "weights": "fp8 e4m3 per-row (layers), fp32 (codebook heads)"}
+    del g, m, head
+    torch.cuda.empty_cache()
     return res
 
 
