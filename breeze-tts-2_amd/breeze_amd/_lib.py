@@ -42,6 +42,7 @@ EXPORTS = (
     "bz_attn_step",
     "bz_attn_workspace",
     "bz_attn_default_split",
+    "bz_sample_cfg",
 )
 
 
@@ -121,6 +122,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.bz_attn_workspace.argtypes = [i32, i32, i32, i32, i32]
     lib.bz_attn_default_split.restype = ctypes.c_int32
     lib.bz_attn_default_split.argtypes = [i32]
+    lib.bz_sample_cfg.restype = ctypes.c_int
+    lib.bz_sample_cfg.argtypes = [vp, i64, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
 
 
 def lib() -> ctypes.CDLL:

@@ -1,5 +1,5 @@
 """The C ABI of libbzgemv.so without a GPU: the library loads, exports every
-function include/bz_gemv.h and include/bz_attn.h declare, the ctypes descriptor matches the C
+function the headers under include/ declare, the ctypes descriptor matches the C
 struct byte for byte, and argument validation answers with the documented
 status codes before anything touches a device."""
 
@@ -15,7 +15,7 @@ import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "bz_gemv.h"
-HEADERS = (HEADER, ROOT / "include" / "bz_attn.h")
+HEADERS = tuple(sorted((ROOT / "include").glob("*.h")))
 
 
 @pytest.fixture(scope="module")
@@ -290,7 +290,7 @@ def test_attn_step_validation(L, kw, status):
 
 
 def test_attn_header_constants(L):
-    text = HEADERS[1].read_text()
+    text = (ROOT / "include" / "bz_attn.h").read_text()
     assert int(re.search(r"#define\s+BZ_MASK_BOOL\s+(\d+)", text).group(1)) == L.MASK_BOOL
     assert int(re.search(r"#define\s+BZ_ATTN_MAX_SPLIT\s+(\d+)", text).group(1)) == 64
 
@@ -330,3 +330,35 @@ def test_head_f32_validation(L):
     assert call(stride=100) == L.ERR_SHAPE                # matrices overlap
     assert call(ldo=2000) == L.ERR_SHAPE
     assert call(w=f + 4) == L.ERR_ALIGNMENT
+
+
+def _sample_args(L, **kw):
+    fake = 1 << 20  # never dereferenced: every case below fails validation
+    a = dict(logits=fake, ld=2051, B=2, V=2051, codec=2048, max_k=1024, guidance=fake, temperature=fake,
+             top_k=fake, top_p=fake, do_sample=fake, seed=fake, counters=fake, tokens=fake, cfg_out=None,
+             probs_out=None, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize(
+    "kw",
+    [
+        {"B": 3},                      # CFG rows come in pairs
+        {"B": 0},
+        {"V": 4097, "ld": 4097},       # wider than the sort
+        {"ld": 2000},                  # row stride below V
+        {"codec": 0},
+        {"codec": 2052},
+        {"max_k": 0},
+        {"max_k": 1025},               # one rank per thread
+        {"V": 64, "ld": 64, "codec": 64, "max_k": 65},  # wider than the vocabulary
+        {"guidance": None},            # CFG needs it
+        {"seed": None},
+        {"counters": None},
+        {"tokens": None},
+        {"logits": None},
+    ],
+)
+def test_sample_validation(L, kw):
+    assert L.lib().bz_sample_cfg(*_sample_args(L, **kw)) == L.ERR_INVALID_ARG
