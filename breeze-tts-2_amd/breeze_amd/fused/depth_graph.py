@@ -22,11 +22,16 @@ CFG layout (models/cudagraph/depth_decoder_graph.py:487-558): rows [0, half)
 are the conditional rows and rows [half, 2 half) the unconditional ones; the
 token sampled from the combined logits goes to both halves.  Sampling follows
 the HF order on the combined logits: invalid codec tokens masked, temperature,
-top-k (a fixed 1024-wide workspace, whose sorted output top-p then works on,
-instead of sorting the whole row again), top-p, softmax, multinomial; rows
-with do_sample = 0 take the argmax of the combined logits.  The sampling
+top-k (a fixed 1024-wide workspace), top-p, softmax, multinomial; rows with
+do_sample = 0 take the argmax of the combined logits.  The sampling
 parameters live in per-row device buffers, so they change between replays
-without a new capture.
+without a new capture.  Two samplers:
+
+    "hip"    (default) one bz_sample_cfg launch per codebook step; its own
+             Philox4x32-10 stream (seed from torch's generator, or `seed`)
+    "torch"  the reference's torch ops (top-k, then top-p over top-k's
+             sorted output instead of a second full sort) and
+             torch.multinomial, i.e. torch's random stream
 """
 
 from __future__ import annotations
@@ -38,6 +43,7 @@ from torch import nn
 from torch.nn import functional as F
 
 from ..heads import Fp32CodebooksHead
+from ..sampling import SampleState, sample_cfg
 from .install import static_cache
 
 __all__ = ["DepthDecodeGraph", "sampling_probs"]
@@ -86,7 +92,13 @@ class DepthDecodeGraph:
     def __init__(self, depth_decoder: nn.Module, *, batch_size: int = 2, temperature: float = 0.9,
                  top_k: int = 50, top_p: float = 1.0, do_sample: bool = True, guidance_scale: float = 3.0,
                  num_codebooks: Optional[int] = None, codec_codebook_size: Optional[int] = None,
-                 debug: bool = False):
+                 debug: bool = False, sampler: str = "hip", seed: Optional[int] = None):
+        if sampler not in ("hip", "torch"):
+            raise ValueError(f"sampler must be 'hip' or 'torch', got {sampler!r}")
+        self.sampler = sampler
+        # the HIP sampler's Philox key: from torch's generator unless given,
+        # so torch.manual_seed makes a run reproducible
+        self._seed = int(seed) if seed is not None else int(torch.randint(0, 2 ** 62, (1,)).item())
         self.depth_model = depth_decoder.model
         head = depth_decoder.codebooks_head
         self.codebooks_head = head if isinstance(head, Fp32CodebooksHead) else Fp32CodebooksHead(head)
@@ -145,6 +157,7 @@ class DepthDecodeGraph:
         self.top_p_buf = torch.full((self.half, 1), d["top_p"], dtype=torch.float32, device=dev)
         self.do_sample_buf = torch.full((self.half,), d["do_sample"], dtype=torch.long, device=dev)
         self.guidance_scale = torch.full((self.half, 1), d["guidance_scale"], dtype=torch.float32, device=dev)
+        self._sample_state = SampleState(self.half, dev, seed=self._seed) if self.sampler == "hip" else None
         # per-codebook combined logits and sampling distributions (debug)
         self.debug_logits = (torch.zeros(self.num_decode_codebooks, self.half, self.vocab_size,
                                          dtype=torch.float32, device=dev) if self.debug else None)
@@ -181,8 +194,25 @@ class DepthDecodeGraph:
             h = h[0] if isinstance(h, tuple) else h
         return self.depth_model.norm(h)
 
+    def reseed(self, seed: int) -> None:
+        """New key for the HIP sampler's stream, draw counters back to zero
+        (the torch sampler follows torch's generator instead)."""
+        self._seed = int(seed)
+        if self._sample_state is not None:
+            self._sample_state.reseed(self._seed)
+
     def _cfg_sample(self, logits: torch.Tensor, i: int) -> None:
         """Combined logits of codebook step i -> self._tok_buf (both halves)."""
+        if self._sample_state is not None:
+            # one launch (bz_sample_cfg): the same filter, its own Philox stream
+            sample_cfg(logits[:, 0, :], self._tok_buf, self._sample_state,
+                       temperature=self.temperature_buf.view(-1), top_k=self.top_k_buf.view(-1),
+                       top_p=self.top_p_buf.view(-1), do_sample=self.do_sample_buf,
+                       guidance=self.guidance_scale.view(-1) if self.batch_size >= 2 else None,
+                       codec_size=self.codec_codebook_size, max_k=self._max_k,
+                       cfg_out=None if self.debug_logits is None else self.debug_logits[i],
+                       probs_out=None if self.debug_probs is None else self.debug_probs[i])
+            return
         half = self.half
         if self.batch_size >= 2:
             cond, uncond = logits[:half, 0, :], logits[half: 2 * half, 0, :]

@@ -16,9 +16,10 @@ fused ones (install_fused_depth) and the head is the fp32 HIP head.
   tests), and each token is the argmax of its logits.
 * Replays of the captured graph, with eager work in between, give exactly
   the eager loop's tokens and logits (every replay checked).
-* Sampling: top-k keeps the sampled token inside the top k of the combined
-  logits, top-p = 0 reduces to the argmax, and the sampling distribution is
-  zero outside the kept set.
+* Sampling, with the HIP sampler and with the torch one: top-k keeps the
+  sampled token inside the top k of the combined logits, top-p = 0 reduces
+  to the argmax, and the sampling distribution is zero outside the kept set;
+  the HIP sampler's draws repeat after a reseed.
 * A batch smaller than the captured one is padded in the CFG layout; a
   larger one recaptures."""
 
@@ -130,11 +131,11 @@ def _rel(a, b):
     return float((a - b).abs().max() / b.abs().max())
 
 
-@pytest.mark.parametrize("captured", [False, True])
-def test_greedy_frames_match_the_cpu_layers(captured):
+@pytest.mark.parametrize("captured,sampler", [(False, "hip"), (True, "hip"), (True, "torch")])
+def test_greedy_frames_match_the_cpu_layers(captured, sampler):
     cfg, dd = _depth_decoder()
     B, gs = 4, 2.5
-    g = _gpu_graph(cfg, dd, B, do_sample=False, guidance_scale=gs)
+    g = _gpu_graph(cfg, dd, B, do_sample=False, guidance_scale=gs, sampler=sampler)
     if captured:
         g.capture(num_warmup=1)
     for seed in (1, 2, 3):
@@ -169,10 +170,11 @@ def test_replays_equal_the_eager_loop():
             _ = (torch.randn(1024, device="cuda") * 2).sum().item()
 
 
-def test_sampling_respects_top_k_and_top_p():
+@pytest.mark.parametrize("sampler", ["hip", "torch"])
+def test_sampling_respects_top_k_and_top_p(sampler):
     cfg, dd = _depth_decoder()
     B = 4
-    g = _gpu_graph(cfg, dd, B, do_sample=True, top_k=3, temperature=1.3, guidance_scale=2.0)
+    g = _gpu_graph(cfg, dd, B, do_sample=True, top_k=3, temperature=1.3, guidance_scale=2.0, sampler=sampler)
     g.capture(num_warmup=1)
     torch.manual_seed(0)
     for seed in range(4):
@@ -196,6 +198,15 @@ def test_sampling_respects_top_k_and_top_p():
     assert torch.equal(toks[0], logits[:, 0].argmax(-1))
     top2 = logits[:, 1].topk(2, dim=-1).indices
     assert all(toks[1, i] in top2[i] for i in range(C - 1))
+    if sampler == "hip":
+        # a reseed repeats the frame's draws exactly; without one they move on
+        bh, first = _inputs(B, 41)
+        g.reseed(77)
+        a = g.run(bh.cuda(), first.cuda(), do_sample=1, top_k=0, top_p=1.0, temperature=3.0).cpu()
+        b = g.run(bh.cuda(), first.cuda()).cpu()
+        g.reseed(77)
+        c = g.run(bh.cuda(), first.cuda()).cpu()
+        assert torch.equal(a, c) and not torch.equal(a, b)
 
 
 def test_smaller_batch_is_padded_and_larger_recaptures():
