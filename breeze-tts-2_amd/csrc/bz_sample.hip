@@ -9,8 +9,11 @@
 //
 //   1. combined logits of the row (and its greedy argmax, first index of the
 //      maximum, as torch.argmax) into LDS, divided by the temperature;
-//   2. a bitonic sort (descending value, ties by ascending index) of the
-//      4096-entry padded row: rank r of the sorted row is rank r of top-k;
+//   2. the k-th largest entry (k = top_k, or the whole workspace) by a radix
+//      select over unique 64-bit keys (scaled value, then ascending index),
+//      and a bitonic sort of just those k entries (padded to a power of two
+//      >= 64; partners under 64 apart trade through wave shuffles): rank r of
+//      the sorted set is rank r of top-k;
 //   3. the top-k ranks (k = top_k, or the whole workspace for top_k <= 0)
 //      and their softmax (one rank per thread, the workspace is <= 1024
 //      wide), an inclusive block scan of it, and the top-p prefix: rank r
@@ -75,9 +78,24 @@ struct SampleParams {
     float* probs_out;
 };
 
-// (value, index) ordering of the sort: larger value first, then smaller index.
-__device__ __forceinline__ bool before(float va, int ia, float vb, int ib) {
-    return va > vb || (va == vb && ia < ib);
+// Sort key of a row entry: the temperature-scaled value mapped to an
+// unsigned order (larger float -> larger key) in the high word, the inverted
+// index in the low word, so keys are unique and a larger key is a larger
+// value, or the same value at a smaller index (the order of torch.argmax).
+__device__ __forceinline__ uint64_t entry_key(float s, int v) {
+    const uint32_t b = __float_as_uint(s);
+    const uint32_t u = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)v);
+}
+__device__ __forceinline__ float key_value(uint64_t key) {
+    const uint32_t u = (uint32_t)(key >> 32);
+    return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
+}
+__device__ __forceinline__ int key_index(uint64_t key) { return (int)(0xFFFFFFFFu - (uint32_t)key); }
+
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, m, 64), hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
+    return ((uint64_t)hi << 32) | lo;
 }
 
 __device__ __forceinline__ float wave_scan_incl(float v, int lane) {
@@ -89,13 +107,15 @@ __device__ __forceinline__ float wave_scan_incl(float v, int lane) {
     return v;
 }
 
+constexpr int kPerThread = kSampleWidth / kSampleThreads;  // row entries a thread holds
+
 __global__ void __launch_bounds__(kSampleThreads) sample_cfg_kernel(SampleParams p) {
-    __shared__ float sv[kSampleWidth];
-    __shared__ int si[kSampleWidth];
+    __shared__ uint64_t cand[kSampleMaxK];  // the selected keys, then sorted
+    __shared__ unsigned hist[256];
     __shared__ float wsum[kSampleThreads / 64];
     __shared__ float wbest_v[kSampleThreads / 64];
     __shared__ int wbest_i[kSampleThreads / 64];
-    __shared__ int greedy_s;
+    __shared__ int greedy_s, ncand, sel_digit, sel_need, sel_count, pick, last_kept;
     const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     constexpr int NW = kSampleThreads / 64;
     const float* cond = p.logits + (int64_t)r * p.ld;
@@ -103,11 +123,14 @@ __global__ void __launch_bounds__(kSampleThreads) sample_cfg_kernel(SampleParams
     const float g = p.B >= 2 ? p.guidance[r] : 0.0f;
     const float temp = p.temperature[r];
 
-    // 1. combined logits, greedy argmax, scaled row into LDS
+    // 1. combined logits, greedy argmax, the scaled entries' keys (registers)
     float best_v = -INFINITY;
     int best_i = 0x7FFFFFFF;
-    for (int v = tid; v < kSampleWidth; v += kSampleThreads) {
-        float s = -INFINITY;
+    uint64_t key[kPerThread];
+#pragma unroll
+    for (int q = 0; q < kPerThread; ++q) {
+        const int v = tid + q * kSampleThreads;
+        key[q] = 0;  // absent (below every entry's key)
         if (v < p.V) {
             float c = cond[v];
             if (p.B >= 2) {
@@ -120,10 +143,8 @@ __global__ void __launch_bounds__(kSampleThreads) sample_cfg_kernel(SampleParams
                 best_v = c;
                 best_i = v;
             }
-            s = c / temp;
+            key[q] = entry_key(c / temp, v);
         }
-        sv[v] = s;
-        si[v] = v;
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -138,7 +159,82 @@ __global__ void __launch_bounds__(kSampleThreads) sample_cfg_kernel(SampleParams
         wbest_v[wave] = best_v;
         wbest_i[wave] = best_i;
     }
+    if (tid == 0) ncand = 0;
+
+    // 2. the k-th largest key (k = top_k, or the whole workspace): radix
+    //    select over 8-bit digits from the top; keys are unique, so exactly k
+    //    keys are >= the result.  A pass whose chosen bucket holds exactly
+    //    the keys still needed ends the search.
+    const int64_t tk = p.top_k[r];
+    const int kk = tk > 0 ? (int)min<int64_t>(tk, p.max_k) : p.max_k;
+    uint64_t prefix = 0, mask = 0;
+    int need = kk;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+        if (tid < 256) hist[tid] = 0u;
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < kPerThread; ++q)
+            if (key[q] != 0 && (key[q] & mask) == prefix) atomicAdd(&hist[(key[q] >> shift) & 255u], 1u);
+        __syncthreads();
+        if (wave == 0) {
+            // lane l covers digits 255 - 4l .. 252 - 4l (top down)
+            unsigned c4[4], sum = 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                c4[q] = hist[255 - 4 * lane - q];
+                sum += c4[q];
+            }
+            unsigned incl = sum;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const unsigned t = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += t;
+            }
+            unsigned above = incl - sum;  // keys in higher digits than this lane's
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (above < (unsigned)need && above + c4[q] >= (unsigned)need) {
+                    sel_digit = 255 - 4 * lane - q;
+                    sel_need = need - (int)above;
+                    sel_count = (int)c4[q];
+                }
+                above += c4[q];
+            }
+        }
+        __syncthreads();
+        prefix |= (uint64_t)sel_digit << shift;
+        mask |= (uint64_t)255u << shift;
+        need = sel_need;
+        if (sel_count == need) break;  // workgroup-uniform
+    }
+
+    // 3. the kk selected keys into LDS, padded with zeros to P (a power of
+    //    two >= 64), then a bitonic sort, descending: partners less than 64
+    //    apart trade through wave shuffles, wider ones through LDS
+    const int P = max(64, 1 << (32 - __clz(kk - 1)));
+#pragma unroll
+    for (int q = 0; q < kPerThread; ++q)
+        if (key[q] != 0 && key[q] >= prefix) cand[atomicAdd(&ncand, 1)] = key[q];
     __syncthreads();
+    uint64_t mine = tid < kk ? cand[tid] : 0;
+    for (int lk = 1; (1 << lk) <= P; ++lk) {
+        const int k = 1 << lk;
+        for (int lj = lk - 1; lj >= 0; --lj) {
+            const int j = 1 << lj;
+            uint64_t theirs;
+            if (j < 64) {
+                theirs = shfl_xor64(mine, j);
+            } else {
+                __syncthreads();
+                if (tid < P) cand[tid] = mine;
+                __syncthreads();
+                theirs = tid < P ? cand[tid ^ j] : 0;
+            }
+            const bool lower = (tid & j) == 0, desc = (tid & k) == 0;
+            const uint64_t hi = mine > theirs ? mine : theirs, lo = mine > theirs ? theirs : mine;
+            if (tid < P) mine = (lower == desc) ? hi : lo;
+        }
+    }
     if (tid == 0) {
         float bv = wbest_v[0];
         int bi = wbest_i[0];
@@ -150,33 +246,14 @@ __global__ void __launch_bounds__(kSampleThreads) sample_cfg_kernel(SampleParams
         greedy_s = bi;
     }
 
-    // 2. bitonic sort of the padded row, descending
-    for (int lk = 1; (1 << lk) <= kSampleWidth; ++lk) {
-        const int k = 1 << lk;
-        for (int lj = lk - 1; lj >= 0; --lj) {
-            const int j = 1 << lj;
-            for (int q = tid; q < kSampleWidth / 2; q += kSampleThreads) {
-                const int i = ((q >> lj) << (lj + 1)) | (q & (j - 1)), l = i + j;
-                const float va = sv[i], vb = sv[l];
-                const int ia = si[i], ib = si[l];
-                const bool down = (i & k) == 0;  // this run ends up descending
-                if (down ? before(vb, ib, va, ia) : before(va, ia, vb, ib)) {
-                    sv[i] = vb;
-                    sv[l] = va;
-                    si[i] = ib;
-                    si[l] = ia;
-                }
-            }
-            __syncthreads();
-        }
-    }
-
-    // 3. top-k softmax weights (thread t = rank t), scan, top-p prefix
-    const int64_t tk = p.top_k[r];
-    const int kk = tk > 0 ? (int)min<int64_t>(tk, p.max_k) : p.max_k;
-    const float m = sv[0];
+    // 4. thread t = rank t: top-k softmax weights, block scan, top-p prefix
     const int t = tid;
-    const float e = (t < kk && sv[t] > -INFINITY) ? expf(sv[t] - m) : 0.0f;
+    const float sv_t = key_value(mine);
+    const int si_t = key_index(mine);
+    __shared__ float m_s;  // rank 0 holds the maximum
+    if (tid == 0) m_s = sv_t;
+    __syncthreads();
+    const float e = (t < kk && sv_t > -INFINITY) ? expf(sv_t - m_s) : 0.0f;
     float inc = wave_scan_incl(e, lane);
     if (lane == 63) wsum[wave] = inc;
     __syncthreads();
@@ -190,12 +267,15 @@ __global__ void __launch_bounds__(kSampleThreads) sample_cfg_kernel(SampleParams
     // kept: rank 0, or the cumulative probability before this rank <= top_p
     const bool kept = t < kk && e > 0.0f && (t == 0 || exc / total <= p.top_p[r]);
     __syncthreads();  // wsum is reused below
-    // the kept total (the kept set is a prefix of ranks)
-    const float ke = kept ? e : 0.0f;
+    const float ke = kept ? e : 0.0f;  // the kept set is a prefix of ranks
     float ks = ke;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) ks += __shfl_xor(ks, o, 64);
     if (lane == 0) wsum[wave] = ks;
+    if (tid == 0) {
+        pick = 0x7FFFFFFF;
+        last_kept = 0;
+    }
     __syncthreads();
     float kept_total = 0.0f;
     for (int w = 0; w < NW; ++w) kept_total += wsum[w];
@@ -204,33 +284,25 @@ __global__ void __launch_bounds__(kSampleThreads) sample_cfg_kernel(SampleParams
         float* pr = p.probs_out + (int64_t)r * p.V;
         for (int v = tid; v < p.V; v += kSampleThreads) pr[v] = 0.0f;
         __syncthreads();
-        if (kept) pr[si[t]] = ke / kept_total;
+        if (kept) pr[si_t] = ke / kept_total;
     }
 
-    // 4. the draw: the first kept rank whose cumulative weight exceeds
+    // 5. the draw: the first kept rank whose cumulative weight exceeds
     //    u * kept_total (kept ranks are a prefix, so their cumulative weight
     //    is `inc`)
-    __shared__ int pick, last_kept;
-    if (tid == 0) {
-        pick = 0x7FFFFFFF;
-        last_kept = 0;
-    }
     const uint64_t cnt = p.counters[r];
     uint32_t c[4] = {(uint32_t)cnt, (uint32_t)(cnt >> 32), (uint32_t)r, 0u};
-    const uint64_t key = *p.seed;
-    philox4x32_10(c, (uint32_t)key, (uint32_t)(key >> 32));
+    const uint64_t keyr = *p.seed;
+    philox4x32_10(c, (uint32_t)keyr, (uint32_t)(keyr >> 32));
     const float u = (float)(c[0] >> 8) * (1.0f / 16777216.0f);
-    __syncthreads();
     if (kept) {
         atomicMax(&last_kept, t);
         if (inc > u * kept_total) atomicMin(&pick, t);
     }
     __syncthreads();
-
-    // 5. the token, to the row and its twin; advance the row's call count
-    if (tid == 0) {
-        const int rank = pick == 0x7FFFFFFF ? last_kept : pick;  // rounding at the top end: the last kept rank
-        int64_t tok = p.do_sample[r] ? (int64_t)si[min(rank, kSampleWidth - 1)] : (int64_t)greedy_s;
+    if (tid == (pick == 0x7FFFFFFF ? last_kept : pick)) {  // rounding at the top end: the last kept rank
+        // 6. the token, to the row and its twin; advance the row's call count
+        int64_t tok = p.do_sample[r] ? (int64_t)si_t : (int64_t)greedy_s;
         tok = tok < 0 ? 0 : (tok >= p.V ? p.V - 1 : tok);
         p.tokens[r] = tok;
         if (p.B >= 2) p.tokens[p.half + r] = tok;
