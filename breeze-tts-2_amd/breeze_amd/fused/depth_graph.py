@@ -15,8 +15,10 @@ token:
 The depth layers are FusedDecoderLayer (install_fused_depth): their GEMVs and
 attention steps run on libbzgemv.so, the two-position start as two causal
 decode steps.  The codebook head is Fp32CodebooksHead (bz_head_f32), which
-picks the codebook's matrix on the GPU from the cache position.  Embeddings,
-projectors, rotary embedding, the final norm and the sampling are torch ops.
+picks the codebook's matrix on the GPU from the cache position.  Bias-free
+embedding projectors run as bf16 GEMVs and the final RMSNorm as bz_rmsnorm;
+the rotary tables of the frame's fixed positions are computed once; the
+embedding lookups are torch ops.
 
 CFG layout (models/cudagraph/depth_decoder_graph.py:487-558): rows [0, half)
 are the conditional rows and rows [half, 2 half) the unconditional ones; the
@@ -45,6 +47,7 @@ from torch.nn import functional as F
 from ..heads import Fp32CodebooksHead
 from ..sampling import SampleState, sample_cfg
 from .install import static_cache
+from .kernels import FusedWeight, rms_gemv, rmsnorm
 
 __all__ = ["DepthDecodeGraph", "sampling_probs"]
 
@@ -68,6 +71,24 @@ def sampling_probs(cfg: torch.Tensor, temperature: torch.Tensor, top_k: torch.Te
     top_vals = torch.where(remove, torch.full_like(top_vals, float("-inf")), top_vals)
     scaled = torch.full_like(scaled, float("-inf")).scatter_(1, top_idx, top_vals)
     return F.softmax(scaled, dim=-1)
+
+
+class _Projector:
+    """A bias-free nn.Linear of the depth stack (the embedding projectors)
+    as one bf16 GEMV launch instead of a library GEMM: [..., K] -> [..., N]."""
+
+    def __init__(self, lin: nn.Linear) -> None:
+        self.fw = FusedWeight(lin.weight.detach().to(torch.bfloat16).contiguous(), 16)
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        y = rms_gemv(x.reshape(-1, x.shape[-1]).to(torch.bfloat16).contiguous(), self.fw)
+        return y.reshape(*x.shape[:-1], self.fw.N)
+
+
+def _gemv_or_module(mod):
+    if type(mod) is nn.Linear and mod.bias is None and mod.in_features % 8 == 0:
+        return _Projector(mod)
+    return mod
 
 
 def _real_batch(batch_size: int) -> int:
@@ -130,6 +151,22 @@ class DepthDecodeGraph:
         self.head_prefill_pos = torch.tensor([1], device=dev)
         self.codebook_offsets = [torch.tensor([i * self.vocab_size], dtype=torch.long, device=dev)
                                  for i in range(self.num_decode_codebooks)]
+        # per-position work that does not change between frames: the
+        # embedding projectors as bf16 GEMVs, the final RMSNorm as one
+        # bz_rmsnorm launch, and the rotary tables of the frame's fixed
+        # positions (the reference recomputes them every step)
+        dm = self.depth_model
+        self._inputs_proj = _gemv_or_module(dm.inputs_embeds_projector)
+        bproj = getattr(dm, "backbone_hidden_state_projector", None)
+        self._backbone_proj = None if bproj is None else _gemv_or_module(bproj)
+        nw, neps = getattr(dm.norm, "weight", None), getattr(dm.norm, "variance_epsilon", None)
+        self._norm_w = None if nw is None or neps is None else nw.detach().to(torch.bfloat16).contiguous()
+        self._norm_eps = None if neps is None else float(neps)
+        with torch.no_grad():
+            z = torch.zeros(1, 2, self.hidden_size, dtype=self.dtype, device=dev)
+            self._pe_start = tuple(t.contiguous() for t in dm.rotary_emb(z, self.prefill_cache_pos.unsqueeze(0)))
+            self._pe_decode = [tuple(t.contiguous() for t in dm.rotary_emb(z[:, :1], pos.unsqueeze(0)))
+                               for pos in self.decode_cache_positions]
         self._defaults = dict(temperature=float(temperature), top_k=int(top_k), top_p=float(top_p),
                               do_sample=1 if do_sample else 0, guidance_scale=float(guidance_scale))
         if not 0 <= self._defaults["top_k"] <= self._max_k:
@@ -192,7 +229,9 @@ class DepthDecodeGraph:
             h = layer(h, attention_mask=mask, position_ids=pos_ids, past_key_values=self.static_cache,
                       use_cache=True, cache_position=cache_pos, position_embeddings=pos_emb)
             h = h[0] if isinstance(h, tuple) else h
-        return self.depth_model.norm(h)
+        if self._norm_w is None:
+            return self.depth_model.norm(h)
+        return rmsnorm(h.reshape(-1, h.shape[-1]), self._norm_w, self._norm_eps).reshape(h.shape)
 
     def reseed(self, seed: int) -> None:
         """New key for the HIP sampler's stream, draw counters back to zero
@@ -240,13 +279,11 @@ class DepthDecodeGraph:
         self.prefill_input_ids[:, 1] = self.first_cb_token_buf
         emb = dm.embed_tokens(self.prefill_input_ids)  # [B, 2, audio]
         bh = self.backbone_hidden_buf
-        proj = getattr(dm, "backbone_hidden_state_projector", None)
-        if proj is not None:
-            bh = proj(bh)
+        if self._backbone_proj is not None:
+            bh = self._backbone_proj(bh)
         emb[:, 0] = bh
-        h = dm.inputs_embeds_projector(emb)  # [B, 2, hidden]
-        pos_emb = dm.rotary_emb(h, self.prefill_cache_pos.unsqueeze(0))
-        h = self._layers(h, self.prefill_attn, self.prefill_cache_pos, pos_emb)
+        h = self._inputs_proj(emb)  # [B, 2, hidden]
+        h = self._layers(h, self.prefill_attn, self.prefill_cache_pos, self._pe_start)
         logits = self.codebooks_head(h[:, 1:, :], cache_position=self.head_prefill_pos)  # [B, 1, vocab] fp32
         self._cfg_sample(logits, 0)
         self._tok_buf.clamp_(0, self.vocab_size - 1)
@@ -254,10 +291,9 @@ class DepthDecodeGraph:
         top = self.num_codebooks * self.vocab_size - 1
         for i in range(1, self.num_decode_codebooks):
             tok = (self._tok_buf + self.codebook_offsets[i]).unsqueeze(1).clamp_(0, top)
-            h = dm.inputs_embeds_projector(dm.embed_tokens(tok))  # [B, 1, hidden]
+            h = self._inputs_proj(dm.embed_tokens(tok))  # [B, 1, hidden]
             cache_pos = self.decode_cache_positions[i - 1]
-            pos_emb = dm.rotary_emb(h, cache_pos.unsqueeze(0))
-            h = self._layers(h, self.decode_attn[i - 1], cache_pos, pos_emb)
+            h = self._layers(h, self.decode_attn[i - 1], cache_pos, self._pe_decode[i - 1])
             logits = self.codebooks_head(h, cache_position=cache_pos)
             self._cfg_sample(logits, i)
             self._tok_buf.clamp_(0, self.vocab_size - 1)
