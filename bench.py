@@ -454,6 +454,10 @@ def pmc_summary(fetch_dir: str, write_dir: str) -> int:
 # GEMV shapes of the benchmark configurations C1-C4
 CONFIG_SHAPES = [
     ("C1 rms->int4 K2048 N2048", "int4", 2048, 2048, 0, True, (1, 2)),
+    # one GPU's share of an 8-way tensor-parallel layer (column-parallel
+    # gate|up [gate_i; up_i], row-parallel down): the same kernels at the shard shape
+    ("E 1/8 shard rms->int4 gate|up K2560 N2x1280 silu", "int4", 2560, 2560, 1, True, (1, 2)),
+    ("E 1/8 shard int4 down K1280 N2560", "int4", 2560, 1280, 0, False, (1, 2)),
     ("C2 rms->int4 gate|up K2560 N2x10240 silu", "int4", 20480, 2560, 1, True, (1, 2)),
     ("C2 int4 down K10240 N2560", "int4", 2560, 10240, 0, False, (1, 2)),
     ("C3 rms->fp8 qkv K2560 N4096", "fp8", 4096, 2560, 0, True, (1, 2)),
