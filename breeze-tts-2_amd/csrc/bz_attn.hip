@@ -178,6 +178,7 @@ __global__ void __launch_bounds__(kRopeThreads) qkv_rope_cache_kernel(
 constexpr int kAttnWaves = 4;
 constexpr int kAttnThreads = 64 * kAttnWaves;
 constexpr int kBlk = 16;           // positions per block (the MFMA's 16 columns)
+constexpr int kUnsplitMax = 192;   // attended positions up to which a call runs unsplit
 constexpr float kNegBig = -1e30f;  // initial running max, as the reference
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -421,7 +422,14 @@ __global__ void __launch_bounds__(kAttnThreads) attn_kernel(AttnParams a) {
     // cache positions [0, min(pos, S - 1)]; none for pos < 0 (output 0)
     const int64_t pos = *a.pos;
     const int kv_len = pos < 0 ? 0 : (pos >= a.S ? a.S : (int)pos + 1);
-    const int per = (kv_len + a.split - 1) / a.split;
+    // Short contexts run unsplit: the workgroup of split 0 takes every
+    // position and writes the output itself; the others leave before any
+    // barrier.  Up to about 192 positions that beats a split plus the
+    // cross-workgroup combine (three serialized memory round trips).  The
+    // choice follows the device position, so a captured graph adapts to it.
+    const int nsp = kv_len <= kUnsplitMax ? 1 : a.split;
+    if (sp >= nsp) return;
+    const int per = (kv_len + nsp - 1) / nsp;
     const int s_lo = sp * per, s_hi = min(s_lo + per, kv_len);
     const bool has_new = FUSED && pos >= s_lo && pos < s_hi;  // this split holds the new token
     const int64_t kv_base = ((int64_t)b * a.HKV + j) * a.S * D;
@@ -674,7 +682,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_kernel(AttnParams a) {
         float at = 0.0f;
         for (int w = 0; w < kAttnWaves; ++w) at += st_acc[w][h][d] * wgt[w][h];
         const float lt = hl[h];
-        if (a.split == 1) {
+        if (nsp == 1) {
             a.out[(int64_t)b * a.ld_out + (int64_t)(j * G + h) * D + d] = f32_to_bf16(lt > 0.0f ? at / lt : 0.0f);
         } else {  // agent-scope stores: coherent across XCDs without an L2 write-back
             float* pp = a.part + ((hq0 + h) * a.split + sp) * (D + 4);
@@ -685,7 +693,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_kernel(AttnParams a) {
             }
         }
     }
-    if (a.split == 1) return;
+    if (nsp == 1) return;
 
     // The last workgroup of (b, j) to finish combines the splits.  Every
     // thread waits until its partial stores have completed (agent-scope
