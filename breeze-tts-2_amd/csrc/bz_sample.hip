@@ -27,6 +27,7 @@
 //   5. the token (sampled, or the argmax when do_sample is 0) to the row and
 //      its unconditional twin; the row's call count is advanced, so graph
 //      replays draw fresh numbers.
+// A greedy row that reports no probabilities stops after step 1.
 //
 // The random stream is this library's own, not torch's: the sampled tokens
 // follow the same distribution as the reference's, not the same sequence.
@@ -160,6 +161,27 @@ __global__ void __launch_bounds__(kSampleThreads) sample_cfg_kernel(SampleParams
         wbest_i[wave] = best_i;
     }
     if (tid == 0) ncand = 0;
+
+    // A greedy row with no probabilities to report needs only the argmax:
+    // skip the select, sort, softmax and draw.  Same token (same reduction
+    // order as below) and the call count advances as on the full path.
+    if (!p.do_sample[r] && !p.probs_out) {
+        __syncthreads();
+        if (tid == 0) {
+            float bv = wbest_v[0];
+            int bi = wbest_i[0];
+            for (int w = 1; w < NW; ++w)
+                if (wbest_v[w] > bv || (wbest_v[w] == bv && wbest_i[w] < bi)) {
+                    bv = wbest_v[w];
+                    bi = wbest_i[w];
+                }
+            const int64_t tok = bi < 0 ? 0 : (bi >= p.V ? p.V - 1 : bi);
+            p.tokens[r] = tok;
+            if (p.B >= 2) p.tokens[p.half + r] = tok;
+            p.counters[r] = p.counters[r] + 1;
+        }
+        return;
+    }
 
     // 2. the k-th largest key (k = top_k, or the whole workspace): radix
     //    select over 8-bit digits from the top; keys are unique, so exactly k

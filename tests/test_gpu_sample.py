@@ -87,6 +87,32 @@ def test_filter_and_greedy_match_torch():
     assert int(tokens[1]) == int(cfg_out[1].argmax()) == int(cfg[1].argmax())
 
 
+def test_greedy_rows_without_probabilities_take_the_argmax_only():
+    """Greedy rows with no probs_out stop after the argmax.  The same mixed
+    batch (half the rows sampled) with and without probs_out, from equal
+    seeds and call counts, gives the same tokens and call counts."""
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    half, V, codec = 16, 2051, 2048
+    logits = torch.randn(2 * half, V, device=DEV, generator=gen) * 3
+    prm = _params(half, temperature=0.8, top_k=50, top_p=0.9)
+    prm["do_sample"][::2] = 0
+    runs = []
+    for probs in (True, False):
+        st = SampleState(half, DEV, seed=11)
+        tokens = torch.full((2 * half,), -1, dtype=torch.int64, device=DEV)
+        cfg_out = torch.empty(half, V, device=DEV)
+        kw = dict(probs_out=torch.empty(half, V, device=DEV)) if probs else {}
+        for _ in range(3):  # three calls: the counters advance on both paths
+            sample_cfg(logits, tokens, st, codec_size=codec, cfg_out=cfg_out, **kw, **prm)
+        torch.cuda.synchronize()
+        runs.append((tokens.clone(), st.counters.clone(), cfg_out))
+    (ta, ca, cfg), (tb, cb, _) = runs
+    assert torch.equal(ta, tb)
+    assert torch.equal(ca, cb)
+    assert torch.equal(tb[0:half:2], cfg[0::2].argmax(-1))
+    assert torch.equal(tb[:half], tb[half:])
+
+
 def test_draws_follow_the_distribution():
     from scipy.stats import chi2
 
