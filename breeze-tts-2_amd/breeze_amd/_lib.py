@@ -16,12 +16,13 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede loading the HIP library)
 
 LIB_PATH = Path(os.environ.get("BZ_LIB", str(Path(__file__).resolve().parent / "libbzgemv.so")))
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # enums of include/bz_gemv.h
 OK = 0
 ERR_INVALID_ARG, ERR_SHAPE, ERR_ALIGNMENT, ERR_UNSUPPORTED, ERR_LAUNCH, ERR_ABI = 1, 2, 3, 4, 5, 6
 W_INT4_ZP, W_INT4_MIN, W_FP8, W_BF16 = 0, 1, 2, 3
+W_INT4_TILED, W_INT4_TILED_PAIRED, W_FP8_TILED, W_FP8_TILED_PAIRED = 4, 5, 6, 7
 EPI_NONE, EPI_SILU_GATE, EPI_RESIDUAL = 0, 1, 2
 DT_BF16, DT_F32 = 0, 1
 MASK_BOOL = 2  # include/bz_attn.h
@@ -36,6 +37,8 @@ EXPORTS = (
     "bz_quantize_int4",
     "bz_quantize_fp8",
     "bz_dequant",
+    "bz_tiled_bytes",
+    "bz_pack_tiled",
     "bz_head_f32",
     "bz_qkv_rope_cache",
     "bz_attn_decode",
@@ -107,6 +110,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.bz_quantize_fp8.argtypes = [vp, i32, i32, i32, f32, vp, vp, vp]
     lib.bz_dequant.restype = ctypes.c_int
     lib.bz_dequant.argtypes = [i32, vp, vp, vp, i32, i32, i32, vp, vp]
+    lib.bz_tiled_bytes.restype = ctypes.c_size_t
+    lib.bz_tiled_bytes.argtypes = [i32, i32, i32]
+    lib.bz_pack_tiled.restype = ctypes.c_int
+    lib.bz_pack_tiled.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, i32, i32, vp]
     lib.bz_head_f32.restype = ctypes.c_int
     lib.bz_head_f32.argtypes = [vp, i64, i32, i32, vp, i32, i64, i32, vp, i64, vp, i64, vp]
     lib.bz_qkv_rope_cache.restype = ctypes.c_int

@@ -29,12 +29,19 @@ from ._lib import (
     EPI_SILU_GATE,
     W_BF16,
     W_FP8,
+    W_FP8_TILED,
+    W_FP8_TILED_PAIRED,
     W_INT4_MIN,
+    W_INT4_TILED,
+    W_INT4_TILED_PAIRED,
     W_INT4_ZP,
 )
 
 __all__ = [
     "gemv",
+    "tiled_bytes",
+    "pack_tiled",
+    "TILED_FORMATS",
     "rmsnorm",
     "silu_mul",
     "quantize_int4_device",
@@ -47,7 +54,13 @@ __all__ = [
     "W_INT4_MIN",
     "W_FP8",
     "W_BF16",
+    "W_INT4_TILED",
+    "W_INT4_TILED_PAIRED",
+    "W_FP8_TILED",
+    "W_FP8_TILED_PAIRED",
 ]
+
+TILED_FORMATS = (W_INT4_TILED, W_INT4_TILED_PAIRED, W_FP8_TILED, W_FP8_TILED_PAIRED)
 
 _DT = {torch.bfloat16: DT_BF16, torch.float32: DT_F32}
 
@@ -135,6 +148,7 @@ def gemv(
     for name, t in (("sc0", sc0), ("sc1", sc1)):
         if t is not None:
             _require_gpu(name, t, dev)
+    _check_weight(w, wfmt, n, K, group, sc0, sc1)
     d = _lib.GemvDesc()
     d.abi_version = _lib.ABI_VERSION
     d.M, d.N, d.K = M, n, K
@@ -146,7 +160,9 @@ def gemv(
     cfg = (tuple(cfg) + (0, 0, 0, 0, 0))[:5]
     if cfg == (0, 0, 0, 0, 0):
         found = _tuning.lookup(dev, n, K, wfmt, epilogue, gamma is not None, M)
-        if found:
+        # an entry forcing a matrix-core path (2, 3, 4) is tuned for int4
+        # group 128 and cannot run a smaller group: the built-in rule decides
+        if found and not (wfmt in (W_INT4_ZP, W_INT4_MIN) and group < 128 and found[3] in (2, 3, 4)):
             cfg = (tuple(found) + (0, 0, 0, 0, 0))[:5]
     d.cfg_depth, d.cfg_waves, d.cfg_tiles, d.cfg_path, d.cfg_slices = cfg
     d.eps = eps
@@ -164,6 +180,95 @@ def gemv(
             ws = _workspace(dev, need)
             d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel() * 4
     _lib.check(_lib.lib().bz_gemv(ctypes.byref(d), _lib.stream_of(x)), "bz_gemv")
+    return out
+
+
+def _weight_spec(wfmt: int, n: int, k: int, group: int):
+    """(bytes of w, (dtype, numel) of sc0 or None, of sc1 or None) a GEMV of
+    this format and shape reads; None when the format is unknown."""
+    if wfmt == W_INT4_ZP:
+        return n * k // 2, (torch.bfloat16, (k // group) * n * 2), None
+    if wfmt == W_INT4_MIN:
+        g = k // group
+        return n * k // 2, (torch.bfloat16, n * g), (torch.bfloat16, n * g)
+    if wfmt == W_FP8:
+        return n * k, (torch.float32, n), None
+    if wfmt == W_BF16:
+        return 2 * n * k, None, None
+    if wfmt in TILED_FORMATS:
+        return tiled_bytes(wfmt, n, k), None, None
+    return None
+
+
+def _check_weight(w, wfmt, n, k, group, sc0, sc1) -> None:
+    """The weight and scale buffers must hold exactly what the kernel reads for
+    (wfmt, n, k, group): a short, mis-shaped or strided buffer would be read
+    past its end on the GPU.  Raises ValueError (the library checks sizes it
+    can see; buffer lengths it cannot)."""
+    if wfmt in (W_INT4_ZP, W_INT4_MIN) and (group <= 0 or k % group):
+        return  # the library reports the shape error
+    spec = _weight_spec(wfmt, n, k, group)
+    if spec is None:
+        return  # unknown format: the library rejects it
+    wbytes, s0, s1 = spec
+    if not w.is_contiguous():
+        raise ValueError("weight buffer must be contiguous")
+    if wfmt in TILED_FORMATS and not wbytes:
+        raise ValueError(f"a {n}x{k} weight cannot be tiled (rows % 16, K % unit)")
+    if w.numel() * w.element_size() != wbytes:
+        raise ValueError(f"weight buffer holds {w.numel() * w.element_size()} bytes, format {wfmt} with "
+                         f"N={n}, K={k} needs {wbytes}")
+    for name, t, want in (("sc0", sc0, s0), ("sc1", sc1, s1)):
+        if want is None:
+            continue
+        if t is None:
+            raise ValueError(f"{name} is required for weight format {wfmt}")
+        dt, numel = want
+        if t.dtype != dt or t.numel() != numel or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous {dt} tensor of {numel} elements for format {wfmt} "
+                             f"(N={n}, K={k}, group={group}); got {t.dtype} {tuple(t.shape)}")
+
+
+def tiled_bytes(wfmt: int, n: int, k: int) -> int:
+    """Bytes of a tiled weight (bz_tiled_bytes); 0 when the shape cannot be tiled."""
+    return int(_lib.lib().bz_tiled_bytes(wfmt, n, k))
+
+
+def pack_tiled(src_wfmt: int, w: torch.Tensor, k: int, dst_wfmt: int, *, sc0: Optional[torch.Tensor] = None,
+               n_total: Optional[int] = None, row0: int = 0, out: Optional[torch.Tensor] = None,
+               group: int = 128) -> torch.Tensor:
+    """Tile the rows of ``w`` (row-major BZ_W_INT4_ZP with scales_zeros
+    ``sc0``, BZ_W_FP8 with row scales ``sc0``, or an unpaired tiled weight)
+    into logical rows [row0, row0 + n) of a ``dst_wfmt`` weight of
+    ``n_total`` rows (default n).  ``out`` (uint8, tiled_bytes bytes) is
+    allocated zero-filled when omitted.  Returns ``out``."""
+    _require_gpu("w", w, w.device)
+    if src_wfmt in (W_INT4_ZP, W_FP8):
+        row_bytes = k // 2 if src_wfmt == W_INT4_ZP else k
+        n = (w.numel() * w.element_size()) // row_bytes
+        if sc0 is None:
+            raise ValueError("a row-major source needs its scales (sc0)")
+        _check_weight(w, src_wfmt, n, k, group, sc0, None)
+    elif src_wfmt in (W_INT4_TILED, W_FP8_TILED):
+        per16 = tiled_bytes(src_wfmt, 16, k)
+        if not per16 or (w.numel() * w.element_size()) % per16:
+            raise ValueError("source is not a whole number of tiled row blocks")
+        n = 16 * (w.numel() * w.element_size()) // per16
+    else:
+        raise ValueError(f"cannot tile from weight format {src_wfmt}")
+    n_total = n if n_total is None else n_total
+    nbytes = tiled_bytes(dst_wfmt, n_total, k)
+    if not nbytes:
+        raise ValueError(f"a {n_total}x{k} weight cannot be tiled as format {dst_wfmt}")
+    if out is None:
+        out = torch.zeros(nbytes, device=w.device, dtype=torch.uint8)
+    elif out.numel() * out.element_size() != nbytes or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous buffer of {nbytes} bytes")
+    _lib.check(
+        _lib.lib().bz_pack_tiled(src_wfmt, w.data_ptr(), _ptr(sc0), n, k, group, dst_wfmt, out.data_ptr(), n_total,
+                                 row0, _lib.stream_of(w)),
+        "bz_pack_tiled",
+    )
     return out
 
 

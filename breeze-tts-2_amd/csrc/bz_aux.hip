@@ -18,6 +18,10 @@
 
 namespace bz {
 
+// the tiled formats' dequantization (bz_tiled.hip)
+bool is_tiled(int wf);
+int dequant_tiled(int wf, const void* w, int N, int K, int group, float* out, hipStream_t st);
+
 __device__ __forceinline__ float load_w(const void* w, int dtype, int64_t i) {
     return dtype == BZ_DT_F32 ? reinterpret_cast<const float*>(w)[i]
                               : bf16_to_f32(reinterpret_cast<const uint16_t*>(w)[i]);
@@ -257,6 +261,8 @@ extern "C" int bz_quantize_fp8(const void* w, int32_t w_dtype, int32_t N, int32_
 extern "C" int bz_dequant(int32_t wfmt, const void* w, const void* sc0, const void* sc1, int32_t N, int32_t K,
                           int32_t group, void* out, void* stream) {
     if (!w || !out || N < 1 || K < 1) return BZ_ERR_INVALID_ARG;
+    if (is_tiled(wfmt))
+        return dequant_tiled(wfmt, w, N, K, group, static_cast<float*>(out), static_cast<hipStream_t>(stream));
     if (wfmt < BZ_W_INT4_ZP || wfmt > BZ_W_BF16) return BZ_ERR_INVALID_ARG;
     const bool i4 = (wfmt == BZ_W_INT4_ZP || wfmt == BZ_W_INT4_MIN);
     if ((i4 || wfmt == BZ_W_FP8) && !sc0) return BZ_ERR_INVALID_ARG;

@@ -91,6 +91,24 @@ __device__ __forceinline__ float sum8(float v) {
     return v;
 }
 
+constexpr int kDppRowMirror = 0x140;     // lane i <- lane 15-i inside each 16-lane row
+
+// Sum / max over each aligned group of 16 lanes (a DPP row); every lane of
+// the group gets it.  After the quad and half-row steps each lane holds its
+// 8-lane group's value; the row mirror pairs the two halves.
+__device__ __forceinline__ float sum16_dpp(float v) {
+    v += dpp_f32<kDppXor1>(v);
+    v += dpp_f32<kDppXor2>(v);
+    v += dpp_f32<kDppHalfMirror>(v);
+    return v + dpp_f32<kDppRowMirror>(v);
+}
+__device__ __forceinline__ float max16_dpp(float v) {
+    v = fmaxf(v, dpp_f32<kDppXor1>(v));
+    v = fmaxf(v, dpp_f32<kDppXor2>(v));
+    v = fmaxf(v, dpp_f32<kDppHalfMirror>(v));
+    return fmaxf(v, dpp_f32<kDppRowMirror>(v));
+}
+
 // Sum over each aligned quad of lanes.
 __device__ __forceinline__ float sum4(float v) {
     v += dpp_f32<kDppXor1>(v);
@@ -113,6 +131,20 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 __device__ __forceinline__ u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// Range-checked 16-byte loads through a buffer resource (V#) covering
+// [p, p + bytes): an offset at or past `bytes` returns zeros and sends no
+// request to memory.  Lets a kernel issue a fixed number of loads
+// unconditionally (exact wait counts) without reading past a buffer or
+// hammering one line with clamped indices.  Word 3 = 0x00020000 is the GFX9
+// untyped-buffer format (data format 32).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+constexpr uint32_t kBufferOob = 0xFFFFFFF0u;  // an offset past any buffer_rsrc range
+__device__ __forceinline__ u32x4 buffer_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 

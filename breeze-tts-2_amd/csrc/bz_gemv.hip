@@ -1,16 +1,17 @@
 // Host dispatcher of the streaming decode GEMV (C ABI entry bz_gemv).  The
 // kernels are in bz_gemv_kernel.h (dot2 path), bz_gemv_mfma.h (bf16
-// matrix-core path), bz_gemv_i8.h (int8 matrix-core path for int4 weights)
-// and bz_gemv_tile.h (several-row tile kernel); their instances live in
-// bz_gemv_{,mfma_,i8_,tile_}<fmt>.hip.
+// matrix-core path), bz_gemv_i8.h (int8 matrix-core path for int4 weights),
+// bz_gemv_tile.h (several-row tile kernel) and bz_gemv_stream.h (the tiled
+// formats' streaming kernel); their instances live in
+// bz_gemv_{,mfma_,i8_,tile_,stream_}<fmt>.hip.
 #include <algorithm>
 
-#include "bz_gemv_i8.h"
+#include "bz_gemv_stream.h"
 #include "bz_gemv_tile.h"
 
 namespace bz {
 
-enum { PATH_DOT2 = 1, PATH_MFMA = 2, PATH_I8 = 3, PATH_TILE = 4 };
+enum { PATH_DOT2 = 1, PATH_MFMA = 2, PATH_I8 = 3, PATH_TILE = 4, PATH_STREAM = 5 };
 
 static int launch_wf(int wf, int path, const GemvParams& p, const Launch& l, hipStream_t st) {
     if (path == PATH_I8) {
@@ -51,10 +52,33 @@ static int check_desc(const bz_gemv_desc* d, DescInfo& di) {
     if (d->abi_version != BZ_ABI_VERSION) return BZ_ERR_ABI;
     const int M = d->M, N = d->N, K = d->K, wf = d->wfmt, epi = d->epilogue;
     if (M < 1 || N < 1 || K < 1) return BZ_ERR_INVALID_ARG;
-    if (wf < BZ_W_INT4_ZP || wf > BZ_W_BF16) return BZ_ERR_INVALID_ARG;
+    if (wf < BZ_W_INT4_ZP || wf > BZ_W_FP8_TILED_PAIRED) return BZ_ERR_INVALID_ARG;
     if (epi < BZ_EPI_NONE || epi > BZ_EPI_RESIDUAL) return BZ_ERR_INVALID_ARG;
     if (d->out_dtype != BZ_DT_BF16 && d->out_dtype != BZ_DT_F32) return BZ_ERR_INVALID_ARG;
     if (!d->x || !d->w || !d->out) return BZ_ERR_INVALID_ARG;
+    if (d->cfg_path < 0 || d->cfg_path > PATH_STREAM || d->cfg_slices < 0) return BZ_ERR_INVALID_ARG;
+    if (is_tiled(wf)) {
+        // tiled formats: scales inside w; 16-row blocks; paired <=> SiLU-gate
+        if (epi == BZ_EPI_RESIDUAL) {
+            if (!d->residual) return BZ_ERR_INVALID_ARG;
+            if (d->residual_dtype != BZ_DT_BF16 && d->residual_dtype != BZ_DT_F32) return BZ_ERR_INVALID_ARG;
+        }
+        if (tiled_paired(wf) != (epi == BZ_EPI_SILU_GATE)) return BZ_ERR_UNSUPPORTED;
+        if (d->cfg_path && d->cfg_path != PATH_STREAM) return BZ_ERR_UNSUPPORTED;
+        if (N % 16 || !tiled_units(wf, K) || (tiled_i4(wf) && d->group != 128)) return BZ_ERR_SHAPE;
+        const int n_out = epi == BZ_EPI_SILU_GATE ? N / 2 : N;
+        if (d->ldx < K || d->ldo < n_out) return BZ_ERR_INVALID_ARG;
+        if (epi == BZ_EPI_RESIDUAL && d->ldr < n_out) return BZ_ERR_INVALID_ARG;
+        if (!aligned(d->x, 16) || (d->ldx % 8) || !aligned(d->w, 16)) return BZ_ERR_ALIGNMENT;
+        if (d->gamma && !aligned(d->gamma, 16)) return BZ_ERR_ALIGNMENT;
+        if (!aligned(d->out, d->out_dtype == BZ_DT_F32 ? 4 : 2)) return BZ_ERR_ALIGNMENT;
+        di.n_out = n_out;
+        di.glog2 = 7;
+        di.row_bytes = tiled_i4(wf) ? K / 2 : K;
+        di.i4 = tiled_i4(wf);
+        return BZ_OK;
+    }
+    if (d->cfg_path == PATH_STREAM) return BZ_ERR_UNSUPPORTED;
     const bool i4 = (wf == BZ_W_INT4_ZP || wf == BZ_W_INT4_MIN);
     if ((i4 || wf == BZ_W_FP8) && !d->sc0) return BZ_ERR_INVALID_ARG;
     if (wf == BZ_W_INT4_MIN && !d->sc1) return BZ_ERR_INVALID_ARG;
@@ -89,7 +113,6 @@ static int check_desc(const bz_gemv_desc* d, DescInfo& di) {
         if (!aligned(d->sc0, 2) || !aligned(d->sc1, 2)) return BZ_ERR_ALIGNMENT;
     }
     if (!aligned(d->out, d->out_dtype == BZ_DT_F32 ? 4 : 2)) return BZ_ERR_ALIGNMENT;
-    if (d->cfg_path < 0 || d->cfg_path > PATH_TILE || d->cfg_slices < 0) return BZ_ERR_INVALID_ARG;
     di.n_out = n_out;
     di.glog2 = glog2;
     di.row_bytes = row_bytes;
@@ -168,6 +191,85 @@ static int launch_tile(int wf, const TileParams& tp, const TileLaunch& l, hipStr
     }
 }
 
+// Launch shape of the tiled streaming kernel for `rows` rows of x (<= 8).
+// Built-in rule (a sweep of 3-16 waves on MI355X over the decode shapes at
+// M = 1, 2): about 4 units (4 KiB of tiles) per wave for int4 and 6 for fp8
+// (e.g. int4 K2560: 5 waves x 4 units; fp8 K2560: 7 x 6), 8 once a row has 64
+// units or more (int4 K10240: 10 x 8), at most 16 waves.
+static int stream_plan(const bz_gemv_desc* d, int rows, StreamLaunch& l) {
+    const int wf = d->wfmt;
+    const int NU = tiled_units(wf, d->K);
+    int nw = d->cfg_waves;
+    if (nw < 0 || nw > kStreamMaxWaves) return BZ_ERR_INVALID_ARG;
+    const int per_wave = NU >= 64 ? 8 : (tiled_i4(wf) ? 4 : 6);
+    if (!nw) nw = std::min(kStreamMaxWaves, (NU + per_wave - 1) / per_wave);
+    const int need = (NU + nw - 1) / nw;
+    int upw = 0;
+    for (int u : kStreamUpw)
+        if (u >= need) {
+            upw = u;
+            break;
+        }
+    if (!upw) return BZ_ERR_UNSUPPORTED;  // K too long for the waves
+    if (!d->cfg_waves) nw = (NU + upw - 1) / upw;
+    l.nw = nw;
+    l.upw = upw;
+    l.mm = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+    l.grid = (unsigned)(d->N / 16);
+    l.lds = (size_t)stream_lds(wf, rows, d->K, nw).total;
+    return l.lds <= (size_t)device_lds_limit() ? BZ_OK : BZ_ERR_UNSUPPORTED;
+}
+
+static int launch_stream(int wf, const StreamParams& p, const StreamLaunch& l, hipStream_t st) {
+    switch (wf) {
+        case WF_I4T: return launch_stream_i4t(p, l, st);
+        case WF_I4TP: return launch_stream_i4tp(p, l, st);
+        case WF_F8T: return launch_stream_f8t(p, l, st);
+        case WF_F8TP: return launch_stream_f8tp(p, l, st);
+        default: return BZ_ERR_INVALID_ARG;
+    }
+}
+
+// The tiled formats: up to kStreamMaxRows rows per launch (fewer when their
+// staged x does not fit the LDS), each launch streaming the weights once.
+static int gemv_tiled(const bz_gemv_desc* d, const DescInfo& di, hipStream_t st) {
+    const int M = d->M;
+    int rows = std::min(M, kStreamMaxRows);
+    StreamLaunch l{};
+    int rc = stream_plan(d, rows, l);
+    while (rc == BZ_ERR_UNSUPPORTED && rows > 1 && l.upw) rc = stream_plan(d, --rows, l);
+    if (rc != BZ_OK) return rc;
+    StreamLaunch l_rem = l;  // the last, shorter launch (planned before anything is launched)
+    if (M > rows && M % rows && stream_plan(d, M % rows, l_rem) != BZ_OK) return BZ_ERR_UNSUPPORTED;
+    StreamParams p;
+    p.ldx = d->ldx;
+    p.w = static_cast<const uint8_t*>(d->w);
+    p.chunk = tiled_chunk_bytes(d->wfmt, tiled_units(d->wfmt, d->K));
+    p.gamma = static_cast<const uint16_t*>(d->gamma);
+    p.ldr = d->ldr;
+    p.ldo = d->ldo;
+    p.eps = d->eps;
+    p.K = d->K;
+    p.NU = tiled_units(d->wfmt, d->K);
+    p.n_out = di.n_out;
+    p.epi = d->epilogue;
+    p.out_f32 = d->out_dtype == BZ_DT_F32;
+    p.res_f32 = d->residual_dtype == BZ_DT_F32;
+    p.norm = d->gamma != nullptr;
+    const size_t osz = p.out_f32 ? 4 : 2, rsz = p.res_f32 ? 4 : 2;
+    for (int m0 = 0; m0 < M; m0 += rows) {
+        const int r = std::min(rows, M - m0);
+        const StreamLaunch& q = r == rows ? l : l_rem;
+        p.M = r;
+        p.x = static_cast<const uint16_t*>(d->x) + (int64_t)m0 * d->ldx;
+        p.out = static_cast<uint8_t*>(d->out) + (int64_t)m0 * d->ldo * osz;
+        p.res = d->residual ? static_cast<const uint8_t*>(d->residual) + (int64_t)m0 * d->ldr * rsz : nullptr;
+        const int lrc = launch_stream(d->wfmt, p, q, st);
+        if (lrc != BZ_OK) return lrc;
+    }
+    return BZ_OK;
+}
+
 }  // namespace bz
 
 using namespace bz;
@@ -175,6 +277,7 @@ using namespace bz;
 extern "C" size_t bz_gemv_workspace(const bz_gemv_desc* d) {
     DescInfo di;
     if (check_desc(d, di) != BZ_OK) return 0;
+    if (is_tiled(d->wfmt)) return 0;
     if (d->cfg_path != PATH_TILE && !tile_auto(d)) return 0;
     TilePlan pl{};
     return tile_plan(d, di, std::min(d->M, kTileMaxRows), pl) == BZ_OK ? pl.ws : 0;
@@ -185,6 +288,7 @@ extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
     const int rc0 = check_desc(d, di);
     if (rc0 != BZ_OK) return rc0;
     const int M = d->M, N = d->N, K = d->K, wf = d->wfmt, epi = d->epilogue;
+    if (is_tiled(wf)) return gemv_tiled(d, di, static_cast<hipStream_t>(stream));
     const int n_out = di.n_out, glog2 = di.glog2;
     const int64_t row_bytes = di.row_bytes;
     const bool i4 = di.i4;

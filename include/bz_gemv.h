@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define BZ_ABI_VERSION 2
+#define BZ_ABI_VERSION 3
 
 typedef enum bz_status {
     BZ_OK = 0,
@@ -53,12 +53,37 @@ typedef enum bz_status {
  *                product (models/fused/kernels.py:124-126,133-134;
  *                Fp8Linear.weight_fp8 / weight_scale, models/fp8_linear.py:62-66).
  * BZ_W_BF16    : w bf16 [N][K]; sc0/sc1 unused (FusedWeight bits=16).
+ *
+ * Tiled formats (the layout the streaming GEMV path reads fastest; written by
+ * bz_pack_tiled, bz_tiled_bytes bytes, N % 16 == 0):
+ *   A row block is 16 weight rows; a unit is 64 bytes of each row (int4: 128
+ *   k = one group of 128; fp8: 64 k).  Row block b occupies one contiguous
+ *   chunk: its K/unit tiles of 1024 bytes (tile u = unit u of the 16 rows, row
+ *   r at byte 64 r, bytes in row-major order), then its scales, padded to a
+ *   multiple of 128 bytes:
+ *     int4: per unit u and row r the (s, z) bf16 pair at byte 64 u + 4 r,
+ *           w_eff = (q - 8) * s + z  (the BZ_W_INT4_ZP semantics, group 128);
+ *     fp8:  the 16 fp32 row scales.
+ *   sc0 / sc1 are unused (the scales travel in w).
+ * BZ_W_INT4_TILED / BZ_W_FP8_TILED: block b holds rows 16b .. 16b+15.
+ * BZ_W_*_TILED_PAIRED: the [gate; up] weight of a SiLU-gate GEMV
+ *   (models/fused/layer.py:60; N = 2 * N_out): block b holds gate rows
+ *   8b .. 8b+7 then up rows 8b .. 8b+7 (logical rows 8b+r and N/2+8b+r), so a
+ *   block finishes 8 outputs silu(g) * u.  Only valid with BZ_EPI_SILU_GATE;
+ *   the unpaired tiled formats do not take that epilogue.
+ * The tiled formats run on GEMV path 5 only (M <= 8 rows per launch; more
+ * rows run as several launches) and need K % 128 == 0 (int4) or
+ * K % 64 == 0 (fp8); int4 group must be 128.
  */
 typedef enum bz_wfmt {
     BZ_W_INT4_ZP = 0,
     BZ_W_INT4_MIN = 1,
     BZ_W_FP8 = 2,
-    BZ_W_BF16 = 3
+    BZ_W_BF16 = 3,
+    BZ_W_INT4_TILED = 4,
+    BZ_W_INT4_TILED_PAIRED = 5,
+    BZ_W_FP8_TILED = 6,
+    BZ_W_FP8_TILED_PAIRED = 7
 } bz_wfmt;
 
 /* Epilogues of models/fused/kernels.py:8-13 (EPI 0/1/2). */
@@ -91,7 +116,9 @@ typedef enum bz_dtype {
  * kernel, 16-column tiles, needs an int4 group >= 128; 3 = int8 MFMA kernel
  * for int4 weights, group >= 128 and K % 128 == 0, x held as two int8
  * planes per row (about 16 significant bits), up to 16 rows per launch;
- * 4 = several-row bf16 MFMA tile kernel, see below).
+ * 4 = several-row bf16 MFMA tile kernel, see below; 5 = the streaming
+ * kernel of the tiled formats, which always take it: there cfg_waves alone
+ * is read, 1..16 waves per row block).
  * Used by tuning sweeps.
  *
  * Several rows (path 4).  Up to 32 rows of x per launch stream every weight
@@ -185,9 +212,31 @@ int bz_quantize_int4(const void* w, int32_t w_dtype, int32_t N, int32_t K,
 int bz_quantize_fp8(const void* w, int32_t w_dtype, int32_t N, int32_t K,
                     float amax_floor, void* codes, void* scale, void* stream);
 
+/* Bytes of a tiled weight (wfmt one of the BZ_W_*_TILED formats) of N rows
+ * and K columns; 0 when the shape cannot be tiled (N % 16, or K not a
+ * multiple of the unit's 128 (int4) / 64 (fp8) values). */
+size_t bz_tiled_bytes(int32_t wfmt, int32_t N, int32_t K);
+
+/* Write logical rows [row0, row0 + n) of a tiled weight of N rows (dst,
+ * bz_tiled_bytes(dst_wfmt, N, K) bytes, 16-byte aligned) from a source of n
+ * rows: row-major BZ_W_INT4_ZP (group 128; src_sc0 = scales_zeros bf16
+ * [K/128][n][2]) or BZ_W_INT4_TILED (n % 16 == 0, src_sc0 unused) for the
+ * int4 tiled formats; BZ_W_FP8 (src_sc0 = float [n] row scales) or
+ * BZ_W_FP8_TILED for the fp8 ones.  For the paired formats logical row r < N/2 is
+ * gate row r and r >= N/2 up row r - N/2, so [gate; up] is packed by one call
+ * over all N rows or by one call per half (row0 = 0, row0 = N/2).  Load-time
+ * work with no counterpart in the reference: it replaces the repack step of
+ * torch._convert_weight_to_int4pack (models/int4_linear.py:59) by this
+ * build's own layout.  Bytes a call does not cover (chunk padding, rows of
+ * other calls) are left as they are. */
+int bz_pack_tiled(int32_t src_wfmt, const void* src_w, const void* src_sc0, int32_t n, int32_t K, int32_t group,
+                  int32_t dst_wfmt, void* dst, int32_t N, int32_t row0, void* stream);
+
 /* Dequantize any weight format to float [N][K] (w_eff of bench_gemv.py:47-52)
  * with the same device unpacking code as bz_gemv.  Used to pin unpacking and
- * indexing bit-exactly, and for checkpoint export. */
+ * indexing bit-exactly, and for checkpoint export.  Tiled formats write the
+ * logical row order (for the paired ones [gate; up]); group must be 128 for
+ * the int4 tiled formats and sc0/sc1 are ignored. */
 int bz_dequant(int32_t wfmt, const void* w, const void* sc0, const void* sc1,
                int32_t N, int32_t K, int32_t group, void* out, void* stream);
 

@@ -25,6 +25,11 @@ the reference's decode linears:
 * ``linear_f32_ref``       fp32 lm_head, models/cudagraph/backbone_graph.py:69-70,273
 * ``codebooks_head_ref``   BreezeCodebooksHead.forward, models/breeze.py:597-612
 * ``rel_err``              bench_gemv.py:53  max|out-ref| / max|ref|
+* ``tile_int4`` / ``tile_fp8`` and their inverses: this build's row-block
+                           tiled weight layout (no reference counterpart: it
+                           replaces tinygemm's opaque repack,
+                           models/int4_linear.py:59), restated byte by byte
+                           from its written definition in include/bz_gemv.h
 
 bfloat16 is handled as raw uint16 bit patterns (numpy has no bf16 dtype).
 Every rounding to bf16 is round-to-nearest-even, as torch's ``.to(bfloat16)``.
@@ -44,6 +49,9 @@ Pinning (what checks each function; see tests/test_oracle.py):
   epilogues    - closed forms of SiLU(g)*u and +residual
   fp32 heads   - torch's CPU float64 linear per codebook (a library routine);
                  codebook selection by one-hot weights naming their codebook
+  tiled layout - untile(tile(x)) = x, every byte of a source lands at the
+                 offset a scalar loop over the definition computes, the paired
+                 order puts gate/up rows 8b+r in tile rows r and 8+r
 No function here is "parity unpinned": the reference publishes no golden
 vectors for this path (it has no automated test of it), so the pins above are
 the mathematics plus committed fixtures produced by this file.
@@ -400,3 +408,92 @@ def synth(n: int, k: int, m: int, seed: int = 0):
     gamma = f32_to_bf16_bits(np.float32(1.0) + rng.standard_normal(k, dtype=np.float32) * np.float32(0.1))
     x = f32_to_bf16_bits(rng.standard_normal((m, k), dtype=np.float32))
     return w, gamma, x
+
+
+# ----------------------------------------------------------------------------
+# Row-block tiled layout (include/bz_gemv.h, BZ_W_*_TILED[_PAIRED])
+# ----------------------------------------------------------------------------
+
+
+def tiled_chunk_bytes(n_units: int, int4: bool) -> int:
+    """Bytes of one 16-row block: n_units tiles of 1024 bytes, then the int4
+    (s, z) pairs (64 bytes per unit) or the 16 fp32 row scales, padded to 128."""
+    raw = n_units * 1024 + (n_units * 64 if int4 else 64)
+    return (raw + 127) // 128 * 128
+
+
+def tiled_row_pos(n_total: int, rows, paired: bool):
+    """(block, row within block) of logical rows ``rows`` of an n_total-row
+    tiled weight.  Paired: gate row r (r < n/2) -> block r//8, row r%8; up row
+    r -> block (r-n/2)//8, row 8 + (r-n/2)%8."""
+    r = np.asarray(rows, dtype=np.int64)
+    if paired:
+        h = n_total // 2
+        rr = np.where(r < h, r, r - h)
+        return rr // 8, rr % 8 + np.where(r < h, 0, 8)
+    return r // 16, r % 16
+
+
+def _tile(rows_bytes, unit_bytes_count, scale_bytes, int4: bool, paired: bool) -> np.ndarray:
+    n = rows_bytes.shape[0]
+    nu = unit_bytes_count
+    chunk = tiled_chunk_bytes(nu, int4)
+    blk, tr = tiled_row_pos(n, np.arange(n), paired)
+    buf = np.zeros((n // 16) * chunk, dtype=np.uint8)
+    base = blk[:, None, None] * chunk + np.arange(nu)[None, :, None] * 1024 + tr[:, None, None] * 64 \
+        + np.arange(64)[None, None, :]
+    buf[base] = rows_bytes.reshape(n, nu, 64)
+    if int4:
+        so = blk[:, None, None] * chunk + nu * 1024 + np.arange(nu)[None, :, None] * 64 + tr[:, None, None] * 4 \
+            + np.arange(4)[None, None, :]
+        buf[so] = scale_bytes  # [n, nu, 4]
+    else:
+        so = blk[:, None] * chunk + nu * 1024 + tr[:, None] * 4 + np.arange(4)[None, :]
+        buf[so] = scale_bytes  # [n, 4]
+    return buf
+
+
+def tile_int4(packed, sz_bits, paired: bool = False) -> np.ndarray:
+    """Row-major even-low nibbles uint8 [N, K/2] + scales_zeros bf16 bits
+    [K/128, N, 2] (group 128) -> the BZ_W_INT4_TILED[_PAIRED] bytes."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    n, half = packed.shape
+    nu = half // 64
+    sz = np.ascontiguousarray(np.asarray(sz_bits, dtype=np.uint16).transpose(1, 0, 2))  # [N, NU, 2]
+    return _tile(packed, nu, sz.view(np.uint8).reshape(n, nu, 4), True, paired)
+
+
+def tile_fp8(codes, scale, paired: bool = False) -> np.ndarray:
+    """Row-major e4m3 codes uint8 [N, K] + fp32 row scales [N] -> the
+    BZ_W_FP8_TILED[_PAIRED] bytes."""
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    n, k = codes.shape
+    sc = np.ascontiguousarray(np.asarray(scale, dtype=np.float32).reshape(n))
+    return _tile(codes, k // 64, sc.view(np.uint8).reshape(n, 4), False, paired)
+
+
+def _untile(buf, n: int, row_bytes: int, int4: bool, paired: bool):
+    nu = row_bytes // 64
+    chunk = tiled_chunk_bytes(nu, int4)
+    buf = np.asarray(buf, dtype=np.uint8)
+    blk, tr = tiled_row_pos(n, np.arange(n), paired)
+    base = blk[:, None, None] * chunk + np.arange(nu)[None, :, None] * 1024 + tr[:, None, None] * 64 \
+        + np.arange(64)[None, None, :]
+    rows = buf[base].reshape(n, row_bytes)
+    if int4:
+        so = blk[:, None, None] * chunk + nu * 1024 + np.arange(nu)[None, :, None] * 64 + tr[:, None, None] * 4 \
+            + np.arange(4)[None, None, :]
+        sz = np.ascontiguousarray(buf[so]).view(np.uint16).reshape(n, nu, 2).transpose(1, 0, 2)
+        return rows, np.ascontiguousarray(sz)
+    so = blk[:, None] * chunk + nu * 1024 + tr[:, None] * 4 + np.arange(4)[None, :]
+    return rows, np.ascontiguousarray(buf[so]).view(np.float32).reshape(n)
+
+
+def untile_int4(buf, n: int, k: int, paired: bool = False):
+    """Inverse of tile_int4: (packed uint8 [N, K/2], scales_zeros bits [K/128, N, 2])."""
+    return _untile(buf, n, k // 2, True, paired)
+
+
+def untile_fp8(buf, n: int, k: int, paired: bool = False):
+    """Inverse of tile_fp8: (codes uint8 [N, K], scale fp32 [N])."""
+    return _untile(buf, n, k, False, paired)

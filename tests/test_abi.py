@@ -109,7 +109,18 @@ def _desc(L, **kw):
     [
         ({"abi_version": 99}, "ERR_ABI"),
         ({"M": 0}, "ERR_INVALID_ARG"),
-        ({"wfmt": 7}, "ERR_INVALID_ARG"),
+        ({"wfmt": 8}, "ERR_INVALID_ARG"),
+        ({"wfmt": 4, "epilogue": 1}, "ERR_UNSUPPORTED"),       # plain tiled + SiLU-gate
+        ({"wfmt": 5}, "ERR_UNSUPPORTED"),                      # paired tiled needs SiLU-gate
+        ({"wfmt": 7}, "ERR_UNSUPPORTED"),
+        ({"wfmt": 4, "N": 72}, "ERR_SHAPE"),                   # 16-row blocks
+        ({"wfmt": 4, "K": 192, "ldx": 192}, "ERR_SHAPE"),      # int4 unit = 128 k
+        ({"wfmt": 4, "group": 64}, "ERR_SHAPE"),               # tiled int4 is group 128
+        ({"wfmt": 6, "K": 160, "ldx": 160}, "ERR_SHAPE"),      # fp8 unit = 64 k
+        ({"wfmt": 4, "cfg_path": 2}, "ERR_UNSUPPORTED"),       # tiled formats run path 5 only
+        ({"cfg_path": 5}, "ERR_UNSUPPORTED"),                  # path 5 reads tiled formats only
+        ({"cfg_path": 6}, "ERR_INVALID_ARG"),
+        ({"wfmt": 4, "w": (1 << 20) + 8}, "ERR_ALIGNMENT"),
         ({"epilogue": 5}, "ERR_INVALID_ARG"),
         ({"out_dtype": 3}, "ERR_INVALID_ARG"),
         ({"x": None}, "ERR_INVALID_ARG"),
@@ -142,6 +153,40 @@ def test_gemv_validation(L, kw, status):
     assert L.lib().bz_gemv(ctypes.byref(d), None) == getattr(L, status)
 
 
+def test_tiled_bytes(L):
+    """Row blocks x chunk: int4 NU x (1024 + 64) bytes, fp8 NU x 1024 + 64,
+    each rounded up to 128; 0 for untileable shapes."""
+    tb = L.lib().bz_tiled_bytes
+    assert tb(L.W_INT4_TILED, 20480, 2560) == 1280 * 20 * 1088
+    assert tb(L.W_INT4_TILED_PAIRED, 20480, 2560) == 1280 * 20 * 1088
+    assert tb(L.W_INT4_TILED, 16, 128) == 1152           # 1088 -> 1152
+    assert tb(L.W_FP8_TILED, 2560, 10240) == 160 * (160 * 1024 + 128)
+    assert tb(L.W_FP8_TILED_PAIRED, 32, 64) == 2 * 1152
+    assert tb(L.W_INT4_TILED, 24, 128) == 0              # rows % 16
+    assert tb(L.W_INT4_TILED, 16, 64) == 0               # K % 128
+    assert tb(L.W_FP8_TILED, 16, 96) == 0                # K % 64
+    assert tb(L.W_INT4_ZP, 16, 128) == 0                 # not a tiled format
+
+
+@pytest.mark.parametrize(
+    "args,status",
+    [
+        ((0, 0, 1 << 20, 16, 256, 128, 4, 1 << 20, 16, 0), "ERR_INVALID_ARG"),   # null source
+        ((0, 1 << 20, 1 << 20, 16, 256, 128, 0, 1 << 20, 16, 0), "ERR_INVALID_ARG"),  # dst not tiled
+        ((2, 1 << 20, 1 << 20, 16, 256, 128, 4, 1 << 20, 16, 0), "ERR_INVALID_ARG"),  # fp8 source, int4 dst
+        ((0, 1 << 20, None, 16, 256, 128, 4, 1 << 20, 16, 0), "ERR_INVALID_ARG"),     # row-major needs scales
+        ((0, 1 << 20, 1 << 20, 16, 256, 128, 4, 1 << 20, 16, 8), "ERR_INVALID_ARG"),  # rows past N
+        ((0, 1 << 20, 1 << 20, 16, 256, 64, 4, 1 << 20, 16, 0), "ERR_SHAPE"),         # group 64
+        ((0, 1 << 20, 1 << 20, 24, 256, 128, 4, 1 << 20, 24, 0), "ERR_SHAPE"),        # N % 16
+        ((4, 1 << 20, None, 8, 256, 128, 5, 1 << 20, 16, 0), "ERR_SHAPE"),            # tiled source rows % 16
+        ((0, (1 << 20) + 4, 1 << 20, 16, 256, 128, 4, 1 << 20, 16, 0), "ERR_ALIGNMENT"),
+        ((0, 1 << 20, (1 << 20) + 2, 16, 256, 128, 4, 1 << 20, 16, 0), "ERR_ALIGNMENT"),
+    ],
+)
+def test_pack_tiled_validation(L, args, status):
+    assert L.lib().bz_pack_tiled(*args, None) == getattr(L, status)
+
+
 def test_gemv_null_descriptor(L):
     assert L.lib().bz_gemv(None, None) == L.ERR_INVALID_ARG
 
@@ -167,7 +212,7 @@ def test_workspace_sizes(L):
 @pytest.mark.parametrize(
     "kw,status",
     [
-        ({"cfg_path": 5}, "ERR_INVALID_ARG"),
+        ({"cfg_path": 6}, "ERR_INVALID_ARG"),
         ({"cfg_path": 4, "M": 8}, "ERR_INVALID_ARG"),                       # split-K needs the workspace
         ({"cfg_path": 4, "M": 8, "workspace": 1 << 20, "workspace_bytes": 100}, "ERR_INVALID_ARG"),
         ({"cfg_path": 4, "M": 8, "cfg_tiles": 3}, "ERR_INVALID_ARG"),

@@ -1,0 +1,328 @@
+"""GPU parity of the tiled weight formats and the streaming GEMV that reads
+them (path 5), through the C ABI, against the CPU oracle.
+
+Bars:
+  * packing, unpacking and indexing: bit-exact (device packer == the
+    oracle's byte-by-byte restatement of the layout; dequantized tiled weights
+    == dequantized row-major weights, bit for bit);
+  * GEMV outputs: max|out-ref|/max|ref| <= 1e-2 (bench_gemv.py:53) against the
+    float64 dequantize-then-matmul oracle on the same packed weights
+    (bench_gemv.py:30-52), <= 4e-3 against the same-rounding oracle (a
+    dropped term or a wrong row fails it), and within one bf16 step (2^-7 of
+    the largest output) of the row-major GEMV of the same weights: both
+    outputs are rounded to bf16, so they may differ by one step.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bz_oracle as O
+from tests._util import Fp8Case, Int4Case, bf16_bits, bf16_tensor, f32, u8_tensor
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+TIGHT = 4e-3
+ONE_BF16_STEP = 2.0 ** -7
+
+from breeze_amd import gemv as G  # noqa: E402
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+def _int4_case(n, k, seed, symmetric=True):
+    w = (_rng(seed).standard_normal((n, k)) * 0.02).astype(np.float32)
+    return Int4Case(w, 128, symmetric=symmetric)
+
+
+def _fp8_case(n, k, seed):
+    w = (_rng(seed).standard_normal((n, k)) * 0.02).astype(np.float32)
+    return Fp8Case(w)
+
+
+def _tiled_i4(c, paired):
+    fmt = G.W_INT4_TILED_PAIRED if paired else G.W_INT4_TILED
+    return G.pack_tiled(G.W_INT4_ZP, c.d_packed, c.K, fmt, sc0=c.d_sz), fmt
+
+
+def _tiled_f8(c, paired):
+    fmt = G.W_FP8_TILED_PAIRED if paired else G.W_FP8_TILED
+    return G.pack_tiled(G.W_FP8, c.d_codes, c.K, fmt, sc0=c.d_scale), fmt
+
+
+# ---------------------------------------------------------------------------
+# layout: bit-exact
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("paired", [False, True])
+@pytest.mark.parametrize("n,k", [(16, 128), (48, 384), (64, 2560)])
+def test_pack_int4_matches_oracle(paired, n, k):
+    c = _int4_case(n, k, 1, symmetric=False)
+    buf, _ = _tiled_i4(c, paired)
+    want = O.tile_int4(c.packed, c.sz_bits, paired)
+    assert np.array_equal(buf.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("paired", [False, True])
+@pytest.mark.parametrize("n,k", [(16, 64), (32, 192), (64, 2560)])
+def test_pack_fp8_matches_oracle(paired, n, k):
+    c = _fp8_case(n, k, 2)
+    buf, _ = _tiled_f8(c, paired)
+    want = O.tile_fp8(c.codes, c.scale, paired)
+    assert np.array_equal(buf.cpu().numpy(), want)
+
+
+def test_pack_halves_and_tiled_source():
+    """[gate; up] packed by one call per half, and re-tiled from the plain
+    tiled buffers of the halves, equals the one-call paired packing."""
+    n, k = 64, 512
+    c = _int4_case(n, k, 3)
+    full = G.pack_tiled(G.W_INT4_ZP, c.d_packed, k, G.W_INT4_TILED_PAIRED, sc0=c.d_sz)
+    h = n // 2
+    gate_sz = bf16_tensor(np.ascontiguousarray(c.sz_bits[:, :h]))
+    up_sz = bf16_tensor(np.ascontiguousarray(c.sz_bits[:, h:]))
+    halves = torch.zeros_like(full)
+    G.pack_tiled(G.W_INT4_ZP, c.d_packed[:h].contiguous(), k, G.W_INT4_TILED_PAIRED, sc0=gate_sz, n_total=n,
+                 out=halves)
+    G.pack_tiled(G.W_INT4_ZP, c.d_packed[h:].contiguous(), k, G.W_INT4_TILED_PAIRED, sc0=up_sz, n_total=n, row0=h,
+                 out=halves)
+    assert torch.equal(full, halves)
+    g_t = G.pack_tiled(G.W_INT4_ZP, c.d_packed[:h].contiguous(), k, G.W_INT4_TILED, sc0=gate_sz)
+    u_t = G.pack_tiled(G.W_INT4_ZP, c.d_packed[h:].contiguous(), k, G.W_INT4_TILED, sc0=up_sz)
+    re = torch.zeros_like(full)
+    G.pack_tiled(G.W_INT4_TILED, g_t, k, G.W_INT4_TILED_PAIRED, n_total=n, out=re)
+    G.pack_tiled(G.W_INT4_TILED, u_t, k, G.W_INT4_TILED_PAIRED, n_total=n, row0=h, out=re)
+    assert torch.equal(full, re)
+
+
+@pytest.mark.parametrize("paired", [False, True])
+def test_dequant_tiled_int4_equals_rowmajor(paired):
+    c = _int4_case(96, 1024, 4, symmetric=False)
+    buf, fmt = _tiled_i4(c, paired)
+    got = f32(G.dequant(fmt, buf, c.N, c.K, group=128))
+    want = f32(G.dequant(G.W_INT4_ZP, c.d_packed, c.N, c.K, sc0=c.d_sz, group=128))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(got.view(np.uint32), c.w_zp.view(np.uint32))
+
+
+@pytest.mark.parametrize("paired", [False, True])
+def test_dequant_tiled_fp8_equals_rowmajor(paired):
+    c = _fp8_case(48, 640, 5)
+    buf, fmt = _tiled_f8(c, paired)
+    got = f32(G.dequant(fmt, buf, c.N, c.K))
+    want = f32(G.dequant(G.W_FP8, c.d_codes, c.N, c.K, sc0=c.d_scale))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_single_nibble_sweep_tiled():
+    """One non-zero nibble at every k of a row, through the tiled decoder:
+    pins k -> (unit, lane piece, byte, nibble) of the tile."""
+    K = 256
+    q = np.zeros((K, K), dtype=np.uint8)
+    q[np.arange(K), np.arange(K)] = np.arange(K) % 15 + 1
+    packed = O.pack_nibbles_even_low(q)
+    sz = O.scales_zeros(np.ones((K, K // 128), np.float32), np.zeros((K, K // 128), np.float32))
+    buf = G.pack_tiled(G.W_INT4_ZP, u8_tensor(packed), K, G.W_INT4_TILED, sc0=bf16_tensor(sz))
+    got = f32(G.dequant(G.W_INT4_TILED, buf, K, K, group=128))
+    assert np.array_equal(got, q.astype(np.float32) - 8.0)
+
+
+# ---------------------------------------------------------------------------
+# GEMV: oracle and row-major path
+# ---------------------------------------------------------------------------
+
+
+def _x(m, k, seed):
+    return O.f32_to_bf16_bits(_rng(seed).standard_normal((m, k)).astype(np.float32))
+
+
+def _gamma(k, seed):
+    return O.f32_to_bf16_bits((1 + 0.1 * _rng(seed).standard_normal(k)).astype(np.float32))
+
+
+def _ref(x_bits, w_eff, gamma_bits, epi, res_bits):
+    xf = O.bf16_bits_to_f32(x_bits)
+    xn = O.rmsnorm_folded(xf, O.bf16_bits_to_f32(gamma_bits)) if gamma_bits is not None else xf
+    res = O.bf16_bits_to_f32(res_bits) if res_bits is not None else None
+    return O.gemv_ref(xn, w_eff, epi, res)
+
+
+def _run_both(fmt_rm, rm_kw, fmt_t, tbuf, n, x_bits, gamma_bits, epi, res_bits):
+    x = bf16_tensor(x_bits)
+    gamma = bf16_tensor(gamma_bits) if gamma_bits is not None else None
+    res = bf16_tensor(res_bits) if res_bits is not None else None
+    out_t = G.gemv(x, tbuf, fmt_t, n, gamma=gamma, epilogue=epi, residual=res)
+    out_r = G.gemv(x, rm_kw.pop("w"), fmt_rm, n, gamma=gamma, epilogue=epi, residual=res, **rm_kw)
+    torch.cuda.synchronize()
+    return f32(out_t), f32(out_r)
+
+
+CASES_I4 = [
+    # (n, k, norm, epilogue)
+    (256, 1024, True, 1),
+    (512, 2048, True, 0),
+    (384, 1280, False, 2),
+    (256, 4096, False, 2),
+    (128, 10240, False, 2),
+]
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 11])
+@pytest.mark.parametrize("n,k,norm,epi", CASES_I4)
+def test_gemv_tiled_int4(m, n, k, norm, epi):
+    c = _int4_case(n, k, 10 + m)
+    buf, fmt = _tiled_i4(c, epi == 1)
+    x_bits = _x(m, k, 20 + m)
+    gamma_bits = _gamma(k, 30) if norm else None
+    n_out = n // 2 if epi == 1 else n
+    res_bits = _x(m, n_out, 40) if epi == 2 else None
+    got, rm = _run_both(G.W_INT4_ZP, {"w": c.d_packed, "sc0": c.d_sz, "group": 128}, fmt, buf, n, x_bits,
+                        gamma_bits, epi, res_bits)
+    ref = _ref(x_bits, c.w_zp, gamma_bits, epi, res_bits)
+    assert O.rel_err(got, ref) <= TIGHT
+    assert O.rel_err(got, rm) <= ONE_BF16_STEP
+
+
+CASES_F8 = [
+    (256, 1024, True, 1),
+    (512, 2560, True, 0),
+    (384, 1280, False, 2),
+    (128, 10240, False, 2),
+]
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 6, 8, 9])
+@pytest.mark.parametrize("n,k,norm,epi", CASES_F8)
+def test_gemv_tiled_fp8(m, n, k, norm, epi):
+    c = _fp8_case(n, k, 50 + m)
+    buf, fmt = _tiled_f8(c, epi == 1)
+    x_bits = _x(m, k, 60 + m)
+    gamma_bits = _gamma(k, 70) if norm else None
+    n_out = n // 2 if epi == 1 else n
+    res_bits = _x(m, n_out, 80) if epi == 2 else None
+    got, rm = _run_both(G.W_FP8, {"w": c.d_codes, "sc0": c.d_scale}, fmt, buf, n, x_bits, gamma_bits, epi,
+                        res_bits)
+    ref = _ref(x_bits, c.w_eff, gamma_bits, epi, res_bits)
+    assert O.rel_err(got, ref) <= TIGHT
+    assert O.rel_err(got, rm) <= ONE_BF16_STEP
+
+
+@pytest.mark.parametrize("waves", [1, 2, 3, 7, 16])
+def test_gemv_tiled_forced_waves(waves):
+    """Every wave count (uneven unit splits, idle waves) gives the same sums;
+    one wave cannot hold the 20 units of a K = 2560 row (10 at most)."""
+    n, k, m = 64, 2560, 2
+    c = _int4_case(n, k, 90)
+    buf, fmt = _tiled_i4(c, False)
+    x = bf16_tensor(_x(m, k, 91))
+    if waves == 1:
+        with pytest.raises(RuntimeError, match="status 4"):
+            G.gemv(x, buf, fmt, n, cfg=(0, waves, 0, 5))
+        return
+    got = f32(G.gemv(x, buf, fmt, n, cfg=(0, waves, 0, 5)))
+    ref = _ref(_x(m, k, 91), c.w_zp, None, 0, None)
+    assert O.rel_err(got, ref) <= TOL
+
+
+def test_gemv_tiled_f32_out_and_residual():
+    n, k, m = 128, 1024, 3
+    c = _fp8_case(n, k, 93)
+    buf, fmt = _tiled_f8(c, False)
+    x_bits = _x(m, k, 94)
+    res = torch.randn(m, n, device="cuda", dtype=torch.float32)
+    out = G.gemv(bf16_tensor(x_bits), buf, fmt, n, epilogue=G.EPI_RESIDUAL, residual=res, out_dtype=torch.float32)
+    ref = O.gemv_ref(O.bf16_bits_to_f32(x_bits), c.w_eff, O.EPI_RES, res.cpu().numpy())
+    assert out.dtype == torch.float32
+    assert O.rel_err(f32(out), ref) <= TOL
+
+
+def test_gemv_tiled_rejects_wrong_epilogue_and_size():
+    n, k = 64, 256
+    c = _int4_case(n, k, 95)
+    plain, _ = _tiled_i4(c, False)
+    paired, _ = _tiled_i4(c, True)
+    x = bf16_tensor(_x(1, k, 96))
+    with pytest.raises(RuntimeError):
+        G.gemv(x, plain, G.W_INT4_TILED, n, epilogue=G.EPI_SILU_GATE)
+    with pytest.raises(RuntimeError):
+        G.gemv(x, paired, G.W_INT4_TILED_PAIRED, n)
+    with pytest.raises(ValueError):
+        G.gemv(x, plain[:-128], G.W_INT4_TILED, n)
+
+
+# ---------------------------------------------------------------------------
+# the benchmark configurations' shapes at full size
+# ---------------------------------------------------------------------------
+
+FULL = [
+    # (name, fmt, n, k, norm, epilogue)
+    ("C2 gate|up", "int4", 20480, 2560, True, 1),
+    ("C2 down", "int4", 2560, 10240, False, 2),
+    ("C3 qkv", "fp8", 4096, 2560, True, 0),
+    ("C3 o_proj", "fp8", 2560, 4096, False, 2),
+    ("C3 gate|up", "fp8", 20480, 2560, True, 1),
+    ("C3 down", "fp8", 2560, 10240, False, 2),
+    ("C5 qkv", "int4", 6144, 2560, True, 0),
+    ("C5 o_proj", "int4", 2560, 4096, False, 2),
+]
+
+
+_FULL_CACHE: dict = {}
+
+
+def _full_case(name, fmt, n, k, epi, seed):
+    if name not in _FULL_CACHE:
+        _FULL_CACHE.clear()  # one full-size weight at a time
+        if fmt == "int4":
+            c = _int4_case(n, k, seed)
+            buf, tf = _tiled_i4(c, epi == 1)
+            _FULL_CACHE[name] = (buf, tf, c.w_zp)
+        else:
+            c = _fp8_case(n, k, seed)
+            buf, tf = _tiled_f8(c, epi == 1)
+            _FULL_CACHE[name] = (buf, tf, c.w_eff)
+    return _FULL_CACHE[name]
+
+
+@pytest.mark.parametrize("name,fmt,n,k,norm,epi", FULL, ids=[f[0] for f in FULL])
+@pytest.mark.parametrize("m", [1, 2])
+def test_gemv_tiled_full_size(name, fmt, n, k, norm, epi, m):
+    seed = sum(name.encode()) % 1000
+    buf, tf, w_eff = _full_case(name, fmt, n, k, epi, seed)
+    x_bits = _x(m, k, seed + 1)
+    gamma_bits = _gamma(k, seed + 2) if norm else None
+    n_out = n // 2 if epi == 1 else n
+    res_bits = _x(m, n_out, seed + 3) if epi == 2 else None
+    out = G.gemv(bf16_tensor(x_bits), buf, tf, n, gamma=bf16_tensor(gamma_bits) if norm else None, epilogue=epi,
+                 residual=bf16_tensor(res_bits) if res_bits is not None else None)
+    ref = _ref(x_bits, w_eff, gamma_bits, epi, res_bits)
+    assert O.rel_err(f32(out), ref) <= TOL
+
+
+def test_gemv_tiled_graph_replays_bit_identical():
+    n, k, m = 2048, 2560, 2
+    c = _int4_case(n, k, 97)
+    buf, fmt = _tiled_i4(c, True)
+    x = bf16_tensor(_x(m, k, 98))
+    gamma = bf16_tensor(_gamma(k, 99))
+    out = torch.empty(m, n // 2, device="cuda", dtype=torch.bfloat16)
+    G.gemv(x, buf, fmt, n, gamma=gamma, epilogue=G.EPI_SILU_GATE, out=out)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(st), torch.cuda.graph(g, stream=st):
+        G.gemv(x, buf, fmt, n, gamma=gamma, epilogue=G.EPI_SILU_GATE, out=out)
+    torch.cuda.current_stream().wait_stream(st)
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)

@@ -472,3 +472,76 @@ def test_planted_mistakes_are_caught():
     res = np.ones((1, 8))
     assert not np.array_equal(gemv_no_res(np.ones((1, 256)), np.zeros((8, 256)), O.EPI_RES, res), res)
     assert np.array_equal(O.gemv_ref(np.ones((1, 256)), np.zeros((8, 256)), O.EPI_RES, res), res)
+
+
+# ---------------------------------------------------------------------------
+# tiled layout (include/bz_gemv.h BZ_W_*_TILED[_PAIRED]): pinned against a
+# scalar loop over its written definition, not the vectorised restatement
+# ---------------------------------------------------------------------------
+
+
+def _tile_scalar(rows_bytes, scales, int4, paired):
+    """Byte-by-byte: logical row r -> block b, row t (paired: gate rows 8b+t,
+    up rows 8b+t-8); unit u of the row at chunk(b) + 1024 u + 64 t; int4 (s, z)
+    at chunk(b) + 1024 NU + 64 u + 4 t, fp8 row scale at chunk(b) + 1024 NU + 4 t."""
+    n, rb = rows_bytes.shape
+    nu = rb // 64
+    chunk = (nu * 1024 + (nu * 64 if int4 else 64) + 127) // 128 * 128
+    buf = bytearray((n // 16) * chunk)
+    for r in range(n):
+        if paired:
+            h = n // 2
+            b, t = ((r // 8, r % 8) if r < h else ((r - h) // 8, 8 + (r - h) % 8))
+        else:
+            b, t = r // 16, r % 16
+        for u in range(nu):
+            for i in range(64):
+                buf[b * chunk + 1024 * u + 64 * t + i] = int(rows_bytes[r, 64 * u + i])
+            if int4:
+                for i in range(4):
+                    buf[b * chunk + 1024 * nu + 64 * u + 4 * t + i] = int(scales[r, u, i])
+        if not int4:
+            for i in range(4):
+                buf[b * chunk + 1024 * nu + 4 * t + i] = int(scales[r, i])
+    return np.frombuffer(bytes(buf), dtype=np.uint8)
+
+
+@pytest.mark.parametrize("paired", [False, True])
+def test_tile_int4_matches_scalar_definition(paired):
+    rng = np.random.default_rng(7)
+    n, k = 32, 256
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    sz = rng.integers(0, 1 << 16, (k // 128, n, 2), dtype=np.uint16)
+    got = O.tile_int4(packed, sz, paired)
+    scales = np.ascontiguousarray(sz.transpose(1, 0, 2)).view(np.uint8).reshape(n, k // 128, 4)
+    assert np.array_equal(got, _tile_scalar(packed, scales, True, paired))
+    p2, s2 = O.untile_int4(got, n, k, paired)
+    assert np.array_equal(p2, packed) and np.array_equal(s2, sz)
+
+
+@pytest.mark.parametrize("paired", [False, True])
+def test_tile_fp8_matches_scalar_definition(paired):
+    rng = np.random.default_rng(8)
+    n, k = 32, 192
+    codes = rng.integers(0, 256, (n, k), dtype=np.uint8)
+    scale = rng.standard_normal(n).astype(np.float32)
+    got = O.tile_fp8(codes, scale, paired)
+    assert np.array_equal(got, _tile_scalar(codes, scale.view(np.uint8).reshape(n, 4), False, paired))
+    c2, s2 = O.untile_fp8(got, n, k, paired)
+    assert np.array_equal(c2, codes) and np.array_equal(s2.view(np.uint32), scale.view(np.uint32))
+
+
+def test_tile_paired_puts_gate_and_up_rows_in_one_block():
+    """Block b of a paired [gate; up] weight holds gate rows 8b..8b+7 in tile
+    rows 0-7 and up rows 8b..8b+7 in tile rows 8-15 (so it yields outputs
+    8b..8b+7), and a chunk is a multiple of 128 bytes."""
+    n, k = 64, 128
+    rows = np.repeat(np.arange(n, dtype=np.uint8)[:, None], k // 2, axis=1)  # row r filled with byte r
+    sz = np.zeros((1, n, 2), dtype=np.uint16)
+    buf = O.tile_int4(rows, sz, paired=True)
+    chunk = O.tiled_chunk_bytes(1, True)
+    assert chunk % 128 == 0 and len(buf) == (n // 16) * chunk
+    for b in range(n // 16):
+        for t in range(16):
+            want = 8 * b + t if t < 8 else n // 2 + 8 * b + t - 8
+            assert buf[b * chunk + 64 * t] == want
