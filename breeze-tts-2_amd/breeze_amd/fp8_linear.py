@@ -13,7 +13,9 @@ definition (bench_gemv.py:49) and its fused path
 ``Fp8Linear.forward`` additionally rounds the activations to fp8 per row
 before ``_scaled_mm`` (models/fp8_linear.py:72-82); that extra rounding is
 not reproduced (it only adds error), since decode here is bound by the weight
-bytes, not by the arithmetic.
+bytes, not by the arithmetic.  Any in_features is accepted, as in the
+reference; rows whose length is not a multiple of 16 are read from a
+zero-padded copy.
 """
 
 from __future__ import annotations
@@ -47,8 +49,6 @@ class Fp8Linear(nn.Module):
         weight = linear.weight.data
         self.in_features = int(weight.shape[1])
         self.out_features = int(weight.shape[0])
-        if self.in_features % 16:
-            raise ValueError(f"in_features {self.in_features} must be a multiple of 16 for the fp8 GEMV")
 
         codes, scale = quantize_fp8_device(weight, AMAX_FLOOR)
         if weight.device.type != "cuda":
@@ -56,16 +56,29 @@ class Fp8Linear(nn.Module):
         self.register_buffer("weight_fp8", codes.contiguous())
         self.register_buffer("weight_scale", scale.reshape(1, -1).contiguous())
 
+    def _gemv_codes(self) -> tuple[torch.Tensor, int]:
+        """(codes uint8, row length) as the GEMV reads them.  The GEMV streams
+        16-byte rows; when in_features is not a multiple of 16 the rows are
+        padded with zero codes (+0.0) in a copy kept beside the reference's
+        buffer and refreshed whenever that buffer changes."""
+        codes = self.weight_fp8.view(torch.uint8)
+        k = self.in_features
+        if k % 16 == 0:
+            return codes, k
+        k16 = -(-k // 16) * 16
+        key = (codes.data_ptr(), codes._version)
+        if getattr(self, "_padded_key", None) != key:
+            self._padded = torch.nn.functional.pad(codes, (0, k16 - k)).contiguous()
+            self._padded_key = key
+        return self._padded, k16
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         shape = x.shape
-        flat = x.reshape(-1, shape[-1])
-        out = gemv_traceable(
-            flat.to(torch.bfloat16),
-            self.weight_fp8.view(torch.uint8),
-            W_FP8,
-            self.out_features,
-            sc0=self.weight_scale,
-        )
+        flat = x.reshape(-1, shape[-1]).to(torch.bfloat16)
+        codes, k = self._gemv_codes()
+        if k != self.in_features:
+            flat = torch.nn.functional.pad(flat, (0, k - self.in_features))
+        out = gemv_traceable(flat, codes, W_FP8, self.out_features, sc0=self.weight_scale)
         return out.to(x.dtype).reshape(*shape[:-1], self.out_features)
 
     def extra_repr(self) -> str:

@@ -44,18 +44,19 @@ def _kind(mod) -> str:
     return type(mod).__name__
 
 
-def _adopt(mods, bits: int) -> FusedWeight:
-    """One FusedWeight over the modules' outputs concatenated along N: the
-    quantized buffers of Int4Linear / Fp8Linear as they are, otherwise the
-    float weights quantized to ``bits`` (16 = bf16)."""
+def _adopt(mods, bits: int, paired: bool = False) -> FusedWeight:
+    """One FusedWeight over the modules' outputs stacked along N: the
+    quantized buffers of Int4Linear / Fp8Linear (re-tiled where the shape
+    allows), otherwise the float weights quantized to ``bits`` (16 = bf16).
+    ``paired``: the two modules are gate and up of a SiLU-gate MLP."""
     kinds = {_kind(m) for m in mods}
     if kinds == {"Int4Linear"}:
-        return FusedWeight.from_int4(*mods)
+        return FusedWeight.from_int4(*mods, paired=paired)
     if kinds == {"Fp8Linear"}:
-        return FusedWeight.from_fp8(*mods)
+        return FusedWeight.from_fp8(*mods, paired=paired)
     if kinds & {"Int4Linear", "Fp8Linear"}:
         raise TypeError(f"cannot fuse a mix of {sorted(kinds)}")
-    return FusedWeight(torch.cat([m.weight for m in mods], 0).detach(), bits)
+    return FusedWeight(torch.cat([m.weight for m in mods], 0).detach(), bits, paired=paired)
 
 
 def _bf16(w):
@@ -80,7 +81,7 @@ class FusedDecoderLayer(nn.Module):
         self.wo = _adopt([attn.o_proj], attn_bits)
         mlp = layer.mlp
         bits = mlp_bits or 16
-        self.wgu = _adopt([mlp.gate_proj, mlp.up_proj], bits)
+        self.wgu = _adopt([mlp.gate_proj, mlp.up_proj], bits, paired=True)
         self.wd = _adopt([mlp.down_proj], bits)
 
     # -- cache helpers (transformers 4.57 and >= 5 StaticLayer) ---------------

@@ -443,6 +443,7 @@ def quantize_fp8_device(weight: torch.Tensor, amax_floor: float):
 def dequant(wfmt: int, w: torch.Tensor, n: int, k: int, *, sc0=None, sc1=None, group: int = 128) -> torch.Tensor:
     """w_eff float32 [n, k] decoded by the GPU path's own unpacking code."""
     _require_gpu("w", w, w.device)
+    _check_weight(w, wfmt, n, k, group, sc0, sc1)
     out = torch.empty(n, k, device=w.device, dtype=torch.float32)
     _lib.check(
         _lib.lib().bz_dequant(wfmt, w.data_ptr(), _ptr(sc0), _ptr(sc1), n, k, group, out.data_ptr(),

@@ -16,14 +16,16 @@ from oracle import bz_oracle as O
 
 from breeze_amd import quantized_checkpoint as Q
 from breeze_amd.fp8_linear import Fp8Linear
-from breeze_amd.int4_linear import LAYOUT, Int4Linear
+from breeze_amd.int4_linear import LAYOUT_ROWMAJOR, LAYOUT_TILED, Int4Linear, tiled_shape
 
 
-def _int4_shell(n, k, g, gen):
+def _int4_shell(n, k, g, gen, tiled=False):
+    """An Int4Linear holding random bytes: tiled [N/16, chunk/4] or row-major [N, K/8]."""
     m = Int4Linear.__new__(Int4Linear)
     nn.Module.__init__(m)
     m.in_features, m.out_features, m.group_size = k, n, g
-    m.register_buffer("weight_int4", torch.randint(-2**31, 2**31 - 1, (n, k // 8), dtype=torch.int32, generator=gen))
+    shape = tiled_shape(n, k) if tiled else (n, k // 8)
+    m.register_buffer("weight_int4", torch.randint(-2**31, 2**31 - 1, shape, dtype=torch.int32, generator=gen))
     m.register_buffer("scales_zeros", torch.randn(k // g, n, 2, generator=gen).to(torch.bfloat16))
     return m
 
@@ -40,27 +42,32 @@ def _fp8_shell(n, k, gen):
 class _Block(nn.Module):
     def __init__(self):
         super().__init__()
-        self.norm = nn.LayerNorm(64)
+        self.norm = nn.LayerNorm(128)
         self.mlp = nn.Module()
-        self.mlp.gate_proj = nn.Linear(64, 256, bias=False)
-        self.mlp.up_proj = nn.Linear(64, 256, bias=False)
-        self.mlp.down_proj = nn.Linear(256, 64, bias=False)
+        self.mlp.gate_proj = nn.Linear(128, 256, bias=False)
+        self.mlp.up_proj = nn.Linear(128, 256, bias=False)
+        self.mlp.down_proj = nn.Linear(256, 128, bias=False)
 
 
 def _quantized_block():
+    """gate: tiled int4 (group 128); up: row-major int4 (group 32); down: fp8."""
     gen = torch.Generator().manual_seed(0)
     blk = _Block()
-    blk.mlp.gate_proj = _int4_shell(256, 64, 32, gen)
-    blk.mlp.up_proj = _int4_shell(256, 64, 32, gen)
-    blk.mlp.down_proj = _fp8_shell(64, 256, gen)
+    blk.mlp.gate_proj = _int4_shell(256, 128, 128, gen, tiled=True)
+    blk.mlp.up_proj = _int4_shell(256, 128, 32, gen)
+    blk.mlp.down_proj = _fp8_shell(128, 256, gen)
     return blk
 
 
 def test_round_trip(tmp_path):
     blk = _quantized_block()
     man = Q.save_quantized(blk, tmp_path, {"int4": "mlp"}, source="synthetic")
-    assert man["modules"]["mlp.gate_proj"]["layout"] == LAYOUT
+    assert man["modules"]["mlp.gate_proj"]["layout"] == LAYOUT_TILED == Q.INT4_LAYOUT
+    assert man["modules"]["mlp.up_proj"]["layout"] == LAYOUT_ROWMAJOR
+    assert man["modules"]["mlp.gate_proj"]["shapes"]["weight_int4"] == list(tiled_shape(256, 128))
     assert man["modules"]["mlp.down_proj"]["kind"] == "fp8"
+    assert man["tensor_count"] == len(blk.state_dict())
+    assert json.loads((tmp_path / Q.MANIFEST_NAME).read_text()) == man
     fresh = _Block()
     manifest = Q.read_manifest(tmp_path)
     assert Q.install_shells(fresh, manifest, "cpu") == 3
@@ -93,10 +100,40 @@ def test_refuses_foreign_layouts_kinds_and_versions(tmp_path):
     int8["modules"]["mlp.up_proj"]["kind"] = "int8"
     with pytest.raises(ValueError, match="not part of this build"):
         Q.install_shells(_Block(), int8, "cpu")
+    unknown = json.loads(json.dumps(man))
+    unknown["modules"]["mlp.gate_proj"]["layout"] = "something-else"
+    with pytest.raises(ValueError, match="tinygemm"):
+        Q.install_shells(_Block(), unknown, "cpu")
     man["version"] = 99
     (tmp_path / Q.MANIFEST_NAME).write_text(json.dumps(man))
     with pytest.raises(ValueError, match="unsupported checkpoint version"):
         Q.read_manifest(tmp_path)
+
+
+@pytest.mark.parametrize("path,key,value", [
+    ("mlp.gate_proj", "weight_int4", [256, 16]),      # a row-major shape under the tiled tag
+    ("mlp.up_proj", "weight_int4", [256, 8]),         # short rows
+    ("mlp.up_proj", "scales_zeros", [2, 256, 2]),     # groups of 64 recorded as 32
+    ("mlp.down_proj", "weight_fp8", [128, 128]),
+    ("mlp.down_proj", "weight_scale", [128]),
+])
+def test_refuses_manifest_shapes_that_do_not_match(tmp_path, path, key, value):
+    """A manifest whose buffer shapes disagree with the module's features
+    and group is refused before any buffer is made: the GEMV would read past
+    a short buffer."""
+    Q.save_quantized(_quantized_block(), tmp_path, {}, source="synthetic")
+    man = Q.read_manifest(tmp_path)
+    man["modules"][path]["shapes"][key] = value
+    with pytest.raises(ValueError, match="do not match"):
+        Q.install_shells(_Block(), man, "cpu")
+
+
+def test_refuses_untileable_tiled_entry(tmp_path):
+    Q.save_quantized(_quantized_block(), tmp_path, {}, source="synthetic")
+    man = Q.read_manifest(tmp_path)
+    man["modules"]["mlp.up_proj"]["layout"] = LAYOUT_TILED      # group 32 has no tiled layout
+    with pytest.raises(ValueError, match="no tiled layout"):
+        Q.install_shells(_Block(), man, "cpu")
 
 
 def test_convert_logical_int4_matches_oracle_packing():

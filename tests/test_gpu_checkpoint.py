@@ -61,6 +61,30 @@ def test_round_trip_forward_identical(tmp_path):
     assert torch.equal(got, ref)
 
 
+def test_rowmajor_checkpoint_is_retiled_on_load(tmp_path):
+    """A checkpoint whose int4 modules hold the row-major layout (tag
+    bz-int4-rowmajor-evenlow-v1) loads onto the GPU re-tiled: the same bytes
+    as a module quantized in the tiled layout, the same outputs."""
+    torch.manual_seed(1)
+    model = _MLP().to("cuda", torch.bfloat16)
+    I4.quantize_module_int4(model, min_bytes=0)
+    x = torch.randn(2, 512, device="cuda").to(torch.bfloat16)
+    ref = model(x)
+    tiled = {n: getattr(model, n).weight_int4.clone() for n in ("gate_proj", "up_proj", "down_proj")}
+    for name, w in tiled.items():
+        mod = getattr(model, name)
+        packed, _ = O.untile_int4(w.view(torch.uint8).cpu().numpy().reshape(-1), mod.out_features, mod.in_features)
+        mod.weight_int4 = torch.from_numpy(packed).view(torch.int32).cuda()
+    man = Q.save_quantized(model, tmp_path, {}, source="synthetic")
+    assert {e["layout"] for e in man["modules"].values()} == {I4.LAYOUT_ROWMAJOR}
+    fresh = _MLP()
+    Q.install_shells(fresh, Q.read_manifest(tmp_path), "meta")
+    Q.load_quantized_state(fresh, tmp_path, "cuda")
+    for name, w in tiled.items():
+        assert torch.equal(getattr(fresh, name).weight_int4, w), name
+    assert torch.equal(fresh(x), ref)
+
+
 def test_module_from_logical_nibbles_matches_oracle():
     rng = np.random.default_rng(4)
     N, K = 512, 1024
@@ -75,6 +99,8 @@ def test_module_from_logical_nibbles_matches_oracle():
     m.register_buffer("weight_int4", w4.cuda())
     m.register_buffer("scales_zeros", sz_t.cuda())
     x = O.round_bf16(rng.standard_normal((2, K)).astype(np.float32))
-    got = f32(m(torch.from_numpy(x).to("cuda", torch.bfloat16)).float())
+    xd = torch.from_numpy(x).to("cuda", torch.bfloat16)
     ref = O.gemv_ref(x, O.dequant_int4_zp(q, sz, 128))
-    assert O.rel_err(got, ref) <= 4e-3
+    assert O.rel_err(f32(m(xd).float()), ref) <= 4e-3
+    assert I4.retile(m) and I4.layout_of(m.weight_int4, N, K) == I4.LAYOUT_TILED
+    assert O.rel_err(f32(m(xd).float()), ref) <= 4e-3

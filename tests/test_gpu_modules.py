@@ -118,21 +118,61 @@ def test_int4_linear_buffers_and_forward(device):
     lin, w = _linear(N, K, 20, device)
     mod = I4.Int4Linear(lin, device="cuda" if device == "cpu" else None)
     assert mod.in_features == K and mod.out_features == N and mod.group_size == 128
-    assert mod.weight_int4.dtype == torch.int32 and tuple(mod.weight_int4.shape) == (N, K // 8)
+    assert mod.weight_int4.dtype == torch.int32 and tuple(mod.weight_int4.shape) == I4.tiled_shape(N, K)
     assert mod.scales_zeros.dtype == torch.bfloat16 and tuple(mod.scales_zeros.shape) == (K // 128, N, 2)
     q, s, lo, z = O.quantize_int4_asym(w, 128)
-    assert np.array_equal(mod.weight_int4.cpu().view(torch.uint8).numpy(), O.pack_nibbles_even_low(q))
     sz = O.scales_zeros(s, z)
     assert np.array_equal(bf16_bits(mod.scales_zeros), sz)
+    tiled = O.tile_int4(O.pack_nibbles_even_low(q), sz)
+    assert np.array_equal(mod.weight_int4.cpu().view(torch.uint8).numpy().reshape(-1), tiled)
     w_eff = O.dequant_int4_zp(q, sz, 128)
-    # M = 1..4 on the row-sliced paths; 5, 12 and 40 (two launches of <= 32 rows) on the tile kernel
+    # M = 1..12 on the streaming kernel (slices of <= 8 rows); 40 and 100 on the prefill branch
     for shape, dtype in (((1, K), torch.bfloat16), ((2, 3, K), torch.bfloat16), ((5, K), torch.float32),
-                         ((2, 6, K), torch.bfloat16), ((40, K), torch.bfloat16)):
+                         ((2, 6, K), torch.bfloat16), ((40, K), torch.bfloat16), ((100, K), torch.float32)):
         x = torch.randn(*shape, generator=torch.Generator().manual_seed(3)).to(dtype)
         y = mod(x.to(_dev()))
         assert y.dtype == dtype and tuple(y.shape) == shape[:-1] + (N,)
         xr = x.to(torch.bfloat16).float().reshape(-1, K).numpy()
         assert O.rel_err(f32(y).reshape(-1, N), O.gemv_ref(xr, w_eff)) <= TOL
+
+
+@pytest.mark.parametrize("group", [32, 64])
+def test_int4_linear_rowmajor_groups(group):
+    """Groups other than 128 keep the row-major layout and its kernels, at
+    decode and several-row M (an int4 table entry forcing a path that needs
+    group 128 must give way to the built-in rule)."""
+    N, K = 2560, 1024
+    lin, w = _linear(N, K, 23 + group, "cuda")
+    mod = I4.Int4Linear(lin, group_size=group)
+    assert tuple(mod.weight_int4.shape) == (N, K // 8)
+    assert I4.layout_of(mod.weight_int4, N, K) == I4.LAYOUT_ROWMAJOR
+    q, s, lo, z = O.quantize_int4_asym(w, group)
+    assert np.array_equal(mod.weight_int4.cpu().view(torch.uint8).numpy(), O.pack_nibbles_even_low(q))
+    w_eff = O.dequant_int4_zp(q, O.scales_zeros(s, z), group)
+    for M in (1, 2, 4, 16):
+        x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).to(torch.bfloat16)
+        y = mod(x.to(_dev()))
+        assert O.rel_err(f32(y), O.gemv_ref(x.float().numpy(), w_eff)) <= TOL, M
+
+
+def test_int4_linear_retile():
+    """A row-major module of a tileable shape, re-tiled in place, computes
+    the same product (the checkpoint loader's conversion of row-major files)."""
+    N, K = 512, 1024
+    lin, w = _linear(N, K, 24, "cuda")
+    ref = I4.Int4Linear(lin)
+    q, s, lo, z = O.quantize_int4_asym(w, 128)
+    mod = I4.Int4Linear.__new__(I4.Int4Linear)
+    nn.Module.__init__(mod)
+    mod.in_features, mod.out_features, mod.group_size = K, N, 128
+    mod.register_buffer("weight_int4", torch.from_numpy(O.pack_nibbles_even_low(q)).view(torch.int32).cuda())
+    mod.register_buffer("scales_zeros", ref.scales_zeros.clone())
+    x = torch.randn(2, K, device=_dev()).to(torch.bfloat16)
+    before = mod(x)
+    assert I4.retile(mod) and not I4.retile(mod)
+    assert torch.equal(mod.weight_int4, ref.weight_int4)
+    assert torch.equal(mod(x), ref(x))
+    assert O.rel_err(f32(before), f32(ref(x))) <= 2.0 ** -7
 
 
 def test_int4_linear_rebuilt_from_buffers():
@@ -195,8 +235,8 @@ def test_quantize_module_int4_converts_large_layers():
     assert got.dtype == torch.float32
     # against the same MLP on the dequantized weights (decode pinned bit-exact
     # by the golden tests), fp32: only the kernel's bf16 activations differ
-    wd = {n: G.dequant(G.W_INT4_ZP, getattr(m, n).weight_int4, getattr(m, n).out_features,
-                       getattr(m, n).in_features, sc0=getattr(m, n).scales_zeros)
+    wd = {n: G.dequant(G.W_INT4_TILED, getattr(m, n).weight_int4, getattr(m, n).out_features,
+                       getattr(m, n).in_features)
           for n in ("gate_proj", "up_proj", "down_proj")}
     h = torch.nn.functional.silu(x @ wd["gate_proj"].t()) * (x @ wd["up_proj"].t())
     assert O.rel_err(f32(got), f32(h @ wd["down_proj"].t())) <= TOL
@@ -233,7 +273,7 @@ def test_quantize_module_fp8_converts_large_layers():
 def test_rms_gemv(bits, epi):
     N, K, M = 512, 1024, 2
     w, gamma, x = O.synth(N, K, M, seed=30 + bits + epi)
-    fw = FK.FusedWeight(torch.from_numpy(w).to(_dev()), bits=bits)
+    fw = FK.FusedWeight(torch.from_numpy(w).to(_dev()), bits=bits, paired=epi == 1)
     xd, gd = bf16_tensor(x), bf16_tensor(gamma)
     n_out = N // 2 if epi == 1 else N
     res = torch.randn(M, n_out, device=_dev()).to(torch.bfloat16) if epi == 2 else None
@@ -246,8 +286,8 @@ def test_rms_gemv(bits, epi):
         assert np.array_equal(bf16_bits(fw.s), s_bits) and np.array_equal(bf16_bits(fw.z), m_bits)
     elif bits == 8:
         codes, scale = O.pack_fp8(w)
-        assert np.array_equal(fw.w.view(torch.uint8).cpu().numpy(), codes)
-        assert np.array_equal(fw.s.cpu().numpy(), scale)
+        assert fw.layout == ("tiled-paired" if epi == 1 else "tiled") and fw.s is None
+        assert np.array_equal(fw.w.cpu().numpy(), O.tile_fp8(codes, scale, paired=epi == 1))
         w_eff = O.dequant_fp8(codes, scale)
     else:
         w_eff = O.round_bf16(w)
@@ -257,33 +297,81 @@ def test_rms_gemv(bits, epi):
     assert O.rel_err(f32(out), ref) <= TOL
 
 
-def test_from_int4_gate_up_silu():
+@pytest.mark.parametrize("paired", [True, False])
+def test_from_int4_gate_up_silu(paired):
     """Two Int4Linear modules fused as [gate; up] with the SiLU-gate epilogue
-    (models/fused/layer.py:56-60, kernels.py:116-127)."""
+    (models/fused/layer.py:56-60, kernels.py:116-127): one launch over the
+    paired tiling, or GEMV + silu_mul over the unpaired one."""
     K, H = 1024, 384
     g_lin, wg = _linear(H, K, 40, "cuda")
     u_lin, wu = _linear(H, K, 41, "cuda")
     gm, um = I4.Int4Linear(g_lin), I4.Int4Linear(u_lin)
-    fw = FK.FusedWeight.from_int4(gm, um)
-    assert fw.N == 2 * H and fw.K == K and fw.layout == "zp"
+    fw = FK.FusedWeight.from_int4(gm, um, paired=paired)
+    assert fw.N == 2 * H and fw.K == K and fw.layout == ("tiled-paired" if paired else "tiled")
+    qg, sg, _, zg = O.quantize_int4_asym(wg, 128)
+    qu, su, _, zu = O.quantize_int4_asym(wu, 128)
+    sz = np.concatenate([O.scales_zeros(sg, zg), O.scales_zeros(su, zu)], axis=1)
+    packed = O.pack_nibbles_even_low(np.concatenate([qg, qu]))
+    assert np.array_equal(fw.w.cpu().numpy(), O.tile_int4(packed, sz, paired=paired))
     _, gamma, x = O.synth(1, K, 2, seed=42)
     out = FK.rms_gemv(bf16_tensor(x), fw, bf16_tensor(gamma), 1e-6, epilogue=FK.EPI_SILU_GATE)
     xn = O.rmsnorm_f32(O.bf16_bits_to_f32(x), O.bf16_bits_to_f32(gamma))
-    qg, sg, _, zg = O.quantize_int4_asym(wg, 128)
-    qu, su, _, zu = O.quantize_int4_asym(wu, 128)
     w_eff = np.concatenate([O.dequant_int4_zp(qg, O.scales_zeros(sg, zg)), O.dequant_int4_zp(qu, O.scales_zeros(su, zu))])
     assert O.rel_err(f32(out), O.gemv_ref(xn, w_eff, O.EPI_SILU)) <= TOL
+    if paired:
+        with pytest.raises(ValueError, match="paired"):
+            FK.rms_gemv(bf16_tensor(x), fw, bf16_tensor(gamma), 1e-6)
 
 
-def test_from_fp8_concat():
-    K = 768
-    mods = [F8.Fp8Linear(_linear(n, K, 50 + i, "cuda")[0]) for i, n in enumerate((256, 64, 64))]
-    fw = FK.FusedWeight.from_fp8(*mods)
-    assert fw.N == 384 and fw.s.shape == (384,)
-    x = torch.randn(1, K, device=_dev()).to(torch.bfloat16)
+def test_from_int4_rowmajor_groups_concat():
+    """Int4Linear modules of group 64 (row-major) are concatenated as they are."""
+    K, H = 1024, 256
+    mods = [I4.Int4Linear(_linear(H, K, 43 + i, "cuda")[0], group_size=64) for i in range(2)]
+    fw = FK.FusedWeight.from_int4(*mods)
+    assert fw.layout == "zp" and fw.group == 64
+    x = torch.randn(2, K, device=_dev()).to(torch.bfloat16)
     out = FK.rms_gemv(x, fw)
     want = torch.cat([m(x) for m in mods], dim=1)
     assert O.rel_err(f32(out), f32(want)) <= 1e-2
+
+
+@pytest.mark.parametrize("paired", [False, True])
+def test_from_fp8_concat(paired):
+    K = 768
+    sizes = (256, 256) if paired else (256, 64, 64)
+    mods = [F8.Fp8Linear(_linear(n, K, 50 + i, "cuda")[0]) for i, n in enumerate(sizes)]
+    fw = FK.FusedWeight.from_fp8(*mods, paired=paired)
+    assert fw.N == sum(sizes) and fw.layout == ("tiled-paired" if paired else "tiled")
+    codes = np.concatenate([m.weight_fp8.view(torch.uint8).cpu().numpy() for m in mods])
+    scale = np.concatenate([m.weight_scale.cpu().numpy()[0] for m in mods])
+    assert np.array_equal(fw.w.cpu().numpy(), O.tile_fp8(codes, scale, paired=paired))
+    x = torch.randn(1, K, device=_dev()).to(torch.bfloat16)
+    if paired:
+        out = FK.rms_gemv(x, fw, epilogue=FK.EPI_SILU_GATE)
+        g, u = (f32(m(x)) for m in mods)
+        want = O.silu(g) * u
+        assert O.rel_err(f32(out), want) <= 1e-2
+    else:
+        out = FK.rms_gemv(x, fw)
+        want = torch.cat([m(x) for m in mods], dim=1)
+        assert O.rel_err(f32(out), f32(want)) <= 1e-2
+
+
+def test_fp8_linear_any_width():
+    """in_features that is not a multiple of 16 (accepted by the reference,
+    models/fp8_linear.py:47-66) runs on zero-padded rows."""
+    N, K = 96, 100
+    lin, w = _linear(N, K, 55, "cuda")
+    mod = F8.Fp8Linear(lin)
+    assert tuple(mod.weight_fp8.shape) == (N, K)
+    codes, scale = O.quantize_fp8_linear(w)
+    assert np.array_equal(mod.weight_fp8.view(torch.uint8).cpu().numpy(), codes)
+    x = torch.randn(3, K, device=_dev()).to(torch.bfloat16)
+    ref = O.gemv_ref(x.float().cpu().numpy(), O.dequant_fp8(codes, scale))
+    assert O.rel_err(f32(mod(x)), ref) <= TOL
+    with torch.no_grad():
+        mod.weight_fp8.copy_(torch.zeros_like(mod.weight_fp8))     # the padded copy follows the buffer
+    assert torch.count_nonzero(mod(x)) == 0
 
 
 def test_rmsnorm_and_silu_mul_kernels():

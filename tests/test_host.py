@@ -37,11 +37,10 @@ def test_int4_rejects_group_mismatch():
         I4.Int4Linear(nn.Linear(288, 16, bias=False), group_size=96)
 
 
-def test_fp8_rejects_bias_and_odd_width():
+def test_fp8_rejects_bias():
+    # any in_features is accepted (models/fp8_linear.py:47-66); only a bias is refused
     with pytest.raises(ValueError, match="Fp8Linear expects a bias-free Linear"):
         F8.Fp8Linear(nn.Linear(256, 16, bias=True))
-    with pytest.raises(ValueError, match="multiple of 16"):
-        F8.Fp8Linear(nn.Linear(100, 16, bias=False))
 
 
 class _Mlp(nn.Module):
@@ -93,14 +92,20 @@ def test_quantize_module_fp8_small_layers():
     assert stats == {"converted": 0, "skipped_below_threshold": 9, "weight_bytes_saved": 0}
 
 
-def test_quantize_module_fp8_errors_propagate():
-    class Odd(nn.Module):
+def test_quantize_module_fp8_errors_propagate(monkeypatch):
+    """quantize_module_fp8 lets a construction error escape (the reference
+    builds Fp8Linear unguarded, models/fp8_linear.py:113)."""
+    class Mlp(nn.Module):
         def __init__(self):
             super().__init__()
-            self.gate_proj = nn.Linear(100, 8, bias=False)
+            self.gate_proj = nn.Linear(96, 8, bias=False)
 
-    with pytest.raises(ValueError):
-        F8.quantize_module_fp8(Odd(), min_bytes=0)
+    def refuse(weight, amax_floor):
+        raise ValueError("refused")
+
+    monkeypatch.setattr(F8, "quantize_fp8_device", refuse)
+    with pytest.raises(ValueError, match="refused"):
+        F8.quantize_module_fp8(Mlp(), min_bytes=0)
 
 
 def test_fused_weight_plumbing():
@@ -120,8 +125,41 @@ def test_fused_weight_plumbing():
     fw.w = torch.zeros(32, 256, dtype=torch.float8_e4m3fn)
     a = fw.gemv_args()
     assert a["wfmt"] == G.W_FP8 and a["w"].dtype == torch.uint8
-    fw.bits, fw.s = 16, None
+    fw.bits, fw.s, fw.layout = 16, None, "bf16"
     assert FK.FusedWeight.gemv_args(fw)["wfmt"] == G.W_BF16
+    fw.w = torch.zeros(2, 1024, dtype=torch.uint8)
+    for bits, layout, wfmt in ((4, "tiled", G.W_INT4_TILED), (4, "tiled-paired", G.W_INT4_TILED_PAIRED),
+                               (8, "tiled", G.W_FP8_TILED), (8, "tiled-paired", G.W_FP8_TILED_PAIRED)):
+        fw.bits, fw.layout = bits, layout
+        a = fw.gemv_args()
+        assert a["wfmt"] == wfmt and a["w"] is fw.w and "sc0" not in a
+    assert fw.nbytes() == 2048
+    c = fw.clone()
+    assert c.layout == fw.layout and c.w is not fw.w and torch.equal(c.w, fw.w)
+
+
+class _Lin:
+    def __init__(self, n, k):
+        self.out_features, self.in_features = n, k
+
+
+def test_stack_shape_rules():
+    assert FK._stack_shape([_Lin(64, 256), _Lin(32, 256)], False) == (96, 256)
+    assert FK._stack_shape([_Lin(64, 256), _Lin(64, 256)], True) == (128, 256)
+    with pytest.raises(ValueError, match="different in_features"):
+        FK._stack_shape([_Lin(64, 256), _Lin(64, 128)], False)
+    with pytest.raises(ValueError, match="paired"):
+        FK._stack_shape([_Lin(64, 256), _Lin(32, 256)], True)
+    with pytest.raises(ValueError, match="paired"):
+        FK._stack_shape([_Lin(64, 256)] * 3, True)
+
+
+def test_int4_layout_rules():
+    assert I4.tileable(2560, 10240, 128) and not I4.tileable(2560, 10240, 64)
+    assert not I4.tileable(24, 256, 128) and not I4.tileable(32, 192, 128)
+    rowmajor = torch.zeros(32, 256 // 8, dtype=torch.int32)
+    assert I4.layout_of(rowmajor, 32, 256) == I4.LAYOUT_ROWMAJOR
+    assert I4.layout_of(torch.zeros(2, 2 * 1024 // 4 + 32, dtype=torch.int32), 32, 256) == I4.LAYOUT_TILED
 
 
 def test_fused_weight_rejects_bits():
