@@ -306,8 +306,16 @@ def test_errors_raise():
     sz = torch.zeros(1, 8, 2, dtype=torch.bfloat16, device=_dev())
     with pytest.raises(RuntimeError, match="unsupported shape"):
         G.gemv(x, w, G.W_INT4_ZP, 8, sc0=sz, group=128)
-    with pytest.raises(RuntimeError, match="invalid argument"):
-        G.gemv(torch.zeros(1, 128, dtype=torch.bfloat16, device=_dev()), w, G.W_INT4_ZP, 8, group=128)
+    x128 = torch.zeros(1, 128, dtype=torch.bfloat16, device=_dev())
+    # buffers that do not hold what the kernel reads are refused before the launch
+    with pytest.raises(ValueError, match="needs 512"):
+        G.gemv(x128, w, G.W_INT4_ZP, 8, sc0=sz, group=128)
+    w_ok = torch.zeros(8, 64, dtype=torch.uint8, device=_dev())
+    with pytest.raises(ValueError, match="sc0 is required"):
+        G.gemv(x128, w_ok, G.W_INT4_ZP, 8, group=128)
+    with pytest.raises(ValueError, match="sc0 must be"):
+        G.gemv(x128, w_ok, G.W_INT4_ZP, 8, sc0=torch.zeros(8, 1, dtype=torch.bfloat16, device=_dev()), group=128,
+               out_dtype=torch.float32)
 
 
 def _table_keys():
