@@ -20,7 +20,8 @@ ABI_VERSION = 3
 
 # enums of include/bz_gemv.h
 OK = 0
-ERR_INVALID_ARG, ERR_SHAPE, ERR_ALIGNMENT, ERR_UNSUPPORTED, ERR_LAUNCH, ERR_ABI = 1, 2, 3, 4, 5, 6
+ERR_INVALID_ARG, ERR_SHAPE, ERR_ALIGNMENT, ERR_UNSUPPORTED, ERR_LAUNCH, ERR_ABI, ERR_SCRATCH = 1, 2, 3, 4, 5, 6, 7
+GEMV_SCRATCH_BYTES = 8 << 20  # BZ_GEMV_SCRATCH_BYTES
 W_INT4_ZP, W_INT4_MIN, W_FP8, W_BF16 = 0, 1, 2, 3
 W_INT4_TILED, W_INT4_TILED_PAIRED, W_FP8_TILED, W_FP8_TILED_PAIRED = 4, 5, 6, 7
 EPI_NONE, EPI_SILU_GATE, EPI_RESIDUAL = 0, 1, 2
@@ -32,6 +33,7 @@ EXPORTS = (
     "bz_strerror",
     "bz_gemv_workspace",
     "bz_gemv",
+    "bz_gemv_noalloc",
     "bz_rmsnorm",
     "bz_silu_mul",
     "bz_quantize_int4",
@@ -100,6 +102,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.bz_gemv_workspace.argtypes = [ctypes.POINTER(GemvDesc)]
     lib.bz_gemv.restype = ctypes.c_int
     lib.bz_gemv.argtypes = [ctypes.POINTER(GemvDesc), vp]
+    lib.bz_gemv_noalloc.restype = ctypes.c_int
+    lib.bz_gemv_noalloc.argtypes = [ctypes.POINTER(GemvDesc), vp]
     lib.bz_rmsnorm.restype = ctypes.c_int
     lib.bz_rmsnorm.argtypes = [vp, i64, vp, f32, vp, i64, i32, i32, vp]
     lib.bz_silu_mul.restype = ctypes.c_int

@@ -213,6 +213,7 @@ extern "C" const char* bz_strerror(int status) {
         case BZ_ERR_UNSUPPORTED: return "request exceeds what this build supports";
         case BZ_ERR_LAUNCH: return "kernel launch failed";
         case BZ_ERR_ABI: return "descriptor abi_version mismatch";
+        case BZ_ERR_SCRATCH: return "call needs more workspace than the static scratch (BZ_GEMV_SCRATCH_BYTES)";
         default: return "unknown status";
     }
 }

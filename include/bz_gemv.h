@@ -34,7 +34,9 @@ typedef enum bz_status {
     BZ_ERR_ALIGNMENT = 3,    /* pointer or leading dimension misaligned    */
     BZ_ERR_UNSUPPORTED = 4,  /* a valid request this build cannot run      */
     BZ_ERR_LAUNCH = 5,       /* the HIP runtime rejected a launch          */
-    BZ_ERR_ABI = 6           /* descriptor abi_version mismatch            */
+    BZ_ERR_ABI = 6,          /* descriptor abi_version mismatch            */
+    BZ_ERR_SCRATCH = 7       /* bz_gemv_noalloc: the call needs more workspace
+                                than BZ_GEMV_SCRATCH_BYTES                  */
 } bz_status;
 
 /* Weight formats.  All weights are row-major over the N output channels.
@@ -178,6 +180,24 @@ size_t bz_gemv_workspace(const bz_gemv_desc* d);
  * Any M >= 1 is accepted (the reference fused kernel stops at M <= 2,
  * models/fused/kernels.py:336). */
 int bz_gemv(const bz_gemv_desc* d, void* stream);
+
+/* Size of bz_gemv_noalloc's static device workspace, per GPU. */
+#define BZ_GEMV_SCRATCH_BYTES ((size_t)8 << 20)
+
+/* bz_gemv without allocation: identical results and kernels, with the
+ * descriptor's workspace fields ignored and replaced by a static device
+ * array of BZ_GEMV_SCRATCH_BYTES that the library holds per GPU until the
+ * process ends.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under graph capture, serving loops and
+ * harnesses that forbid hipMalloc), which otherwise would have to pass a
+ * workspace.  Allocates nothing (no hipMalloc, no library allocation).
+ * Returns BZ_ERR_SCRATCH when bz_gemv_workspace(d) exceeds
+ * BZ_GEMV_SCRATCH_BYTES, else what bz_gemv returns.  The first call on a
+ * device looks up that device's copy of the array and clears its counters
+ * on `stream`.  All calls on one GPU share its array: calls that overlap in
+ * time on one GPU (concurrent streams, host threads) race and must not be
+ * made. */
+int bz_gemv_noalloc(const bz_gemv_desc* d, void* stream);
 
 /* Row RMSNorm, out = bf16(x * rsqrt(mean(x^2)+eps) * gamma); bf16 in/out.
  * Replaces rmsnorm / rmsnorm_kernel, models/fused/kernels.py:541-557. */

@@ -67,8 +67,8 @@ def test_enum_values_match_header(L):
 
 def test_strerror(L):
     lib = L.lib()
-    msgs = [lib.bz_strerror(i).decode() for i in range(7)]
-    assert msgs[0] == "ok" and len(set(msgs)) == 7
+    msgs = [lib.bz_strerror(i).decode() for i in range(8)]
+    assert msgs[0] == "ok" and len(set(msgs)) == 8
     assert lib.bz_strerror(99).decode() == "unknown status"
 
 
@@ -407,3 +407,20 @@ def _sample_args(L, **kw):
 )
 def test_sample_validation(L, kw):
     assert L.lib().bz_sample_cfg(*_sample_args(L, **kw)) == L.ERR_INVALID_ARG
+
+
+def test_gemv_noalloc_refuses_before_touching_the_gpu(L):
+    """bz_gemv_noalloc checks the descriptor version and its workspace need
+    against BZ_GEMV_SCRATCH_BYTES before any HIP call: both refusals work
+    without a GPU."""
+    lib = L.lib()
+    assert lib.bz_gemv_noalloc(None, None) == L.ERR_INVALID_ARG
+    assert lib.bz_gemv_noalloc(ctypes.byref(_desc(L, abi_version=99)), None) == L.ERR_ABI
+    # forced split-K tile path whose partials (4 slices x 32 x 20480 fp32) exceed 8 MiB
+    big = _desc(L, M=32, N=20480, K=2560, ldx=2560, ldo=20480, cfg_path=4, cfg_slices=4)
+    assert lib.bz_gemv_workspace(ctypes.byref(big)) > L.GEMV_SCRATCH_BYTES
+    assert lib.bz_gemv_noalloc(ctypes.byref(big), None) == L.ERR_SCRATCH
+    assert "BZ_GEMV_SCRATCH_BYTES" in lib.bz_strerror(L.ERR_SCRATCH).decode()
+    header = HEADER.read_text()
+    assert re.search(r"#define BZ_GEMV_SCRATCH_BYTES \(\(size_t\)8 << 20\)", header)
+    assert L.GEMV_SCRATCH_BYTES == 8 << 20
