@@ -5,9 +5,11 @@ Workload (the int4 decoder-MLP GEMVs at M = 1): every step runs
   gate|up  RMSNorm -> int4 group-128 GEMV K=2560, N=2x10240 -> SiLU(gate)*up
   down     int4 group-128 GEMV K=10240, N=2560
 on synthetic weights N(0, 0.02) quantized symmetric int4 (bf16 scales), bf16
-activations N(0, 1), gamma = 1 + N(0, 0.1), eps 1e-6, seed 0.  The weights
-rotate over copies spanning >= 1 GiB so every step streams them from HBM,
-and the K timed steps are one HIP-graph replay.
+activations N(0, 1), gamma = 1 + N(0, 0.1), eps 1e-6, seed 0, held in the
+decode layout the modules use (16-row tiled blocks; gate|up paired for the
+SiLU-gate epilogue).  The weights rotate over copies spanning >= 1 GiB so
+every step streams them from HBM, and the K timed steps are one HIP-graph
+replay.
 
 value = algorithmic bytes of K steps / their GPU time, in TB/s, where one
 call's algorithmic bytes are packed weights + scales + x + gamma + output
@@ -17,18 +19,22 @@ call's algorithmic bytes are packed weights + scales + x + gamma + output
                HBM bytes per launch measured by rocprofv3 counters when a
                committed summary holds them;
   cpu_baseline the same MLP step as dequantize-then-matmul in torch on the
-               host cores (a bounded sample of steps);
-  detail       per-kernel times, the full synthetic decode step (26 int4
+               host cores (a bounded sample of steps), and the same step on
+               weights dequantized once;
+  detail       per-kernel times in both weight layouts, the launch and
+               streaming-read floors, the full synthetic decode step (26 int4
                decoder layers + bf16 head) in µs against its bytes-moved
-               roofline, the C1-C4 GEMV table, the fused attention step and
-               the fp32 heads, each against its HBM roofline.
+               roofline, the C1-C4 GEMV table, torch's bf16 linear at the
+               C2/C3 shapes, the fused attention step and the fp32 heads,
+               each against its HBM roofline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-step]
 
-Counter runs (HBM bytes per launch of the gate|up GEMV, scaled by what the
-same counter reads for a plain 256 MiB elementwise copy):
-  rocprofv3 --pmc FETCH_SIZE --output-format csv -d D1 -o run -- python3 bench.py --profile-gateup
-  rocprofv3 --pmc WRITE_SIZE --output-format csv -d D2 -o run -- python3 bench.py --profile-gateup
+Counter runs (HBM bytes per launch of the PROFILE_CASES GEMVs -- the M=1
+decode GEMVs and the C4 split-K tile GEMV -- scaled by what the same counter
+reads for a plain 256 MiB elementwise copy):
+  rocprofv3 --pmc FETCH_SIZE --output-format csv -d D1 -o run -- python3 bench.py --profile-gemvs
+  rocprofv3 --pmc WRITE_SIZE --output-format csv -d D2 -o run -- python3 bench.py --profile-gemvs
   python3 bench.py --pmc-summary D1 D2      (prints the traffic summary)
 
 Matrix-core use of the several-row tile GEMVs (C4 shapes at M = 16 and 32):
@@ -57,7 +63,7 @@ MI355X_SIMDS = 256 * 4
 MI355X_CLOCK_GHZ = 2.4
 GROUP = 128
 EPS = 1e-6
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_int4_gateup_k2560_n20480_m1_traffic.txt")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_decode_traffic.txt")
 COPY_BYTES = 256 << 20
 
 
@@ -79,17 +85,69 @@ def algo_bytes(wbits: int, n: int, k: int, m: int, norm: bool, epi: int) -> int:
 
 
 def read_traffic():
-    """HBM bytes per launch of the gate|up GEMV from the committed rocprofv3
-    counter summary (line 'traffic_bytes_per_launch: <int>'), else None."""
+    """HBM bytes per launch of the gate|up GEMV (the first PROFILE_CASES
+    entry) from the committed rocprofv3 counter summary (line
+    'traffic_bytes_per_launch[<case>]: <int>'), else None."""
+    want = PROFILE_CASES[0][0]
     try:
         with open(TRAFFIC_FILE) as f:
             for line in f:
-                m = re.match(r"\s*traffic_bytes_per_launch:\s*(\d+)", line)
-                if m:
-                    return int(m.group(1))
+                m = re.match(r"\s*traffic_bytes_per_launch\[(.*)\]:\s*(\d+)", line)
+                if m and m.group(1) == want:
+                    return int(m.group(2))
     except OSError:
         pass
     return None
+
+
+# (name, format "int4"/"fp8", layout, N, K, M, epilogue, RMSNorm): the GEMVs
+# whose HBM traffic the counter runs measure, launched PROFILE_REPS times
+# each (after one warm-up launch) in this order by --profile-gemvs.
+PROFILE_CASES = [
+    ("int4 gate|up K2560 N20480 M1", "int4", "tiled", 20480, 2560, 1, 1, True),
+    ("int4 down K10240 N2560 M1", "int4", "tiled", 2560, 10240, 1, 0, False),
+    ("fp8 gate|up K2560 N20480 M1", "fp8", "tiled", 20480, 2560, 1, 1, True),
+    ("fp8 down K10240 N2560 M1", "fp8", "tiled", 2560, 10240, 1, 0, False),
+    ("int4 qkv K2560 N6144 M1", "int4", "tiled", 6144, 2560, 1, 0, True),
+    ("int4 o_proj K4096 N2560 M1", "int4", "tiled", 2560, 4096, 1, 2, False),
+    ("int4 C4 K10240 N2560 M32 (row-major, split-K tile)", "int4", "rowmajor", 2560, 10240, 32, 0, False),
+]
+PROFILE_REPS = 12
+
+
+def profile_gemvs(torch, G, dev) -> int:
+    """Launch each PROFILE_CASES GEMV 1 + PROFILE_REPS times, rotating over
+    copies that span >= 1 GiB, then a 256 MiB elementwise copy three times,
+    for rocprofv3 counter runs; --pmc-summary reads them back."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    for name, fmt, layout, N, K, M, epi, norm in PROFILE_CASES:
+        w = torch.randn(N, K, device=dev, generator=gen) * 0.02
+        base, wfmt, _ = _weights(torch, G, fmt, N, K, epi, w, layout)
+        del w
+        wbytes = sum(t.numel() * t.element_size() for t in base)
+        ncopy = max(2, -(-(1 << 30) // wbytes))
+        copies = [tuple(t.clone() for t in base) for _ in range(ncopy)]
+        x = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
+        gamma = (1 + 0.1 * torch.randn(K, device=dev, generator=gen)).to(torch.bfloat16) if norm else None
+        n_out = N // 2 if epi == 1 else N
+        res = torch.randn(M, n_out, device=dev, generator=gen).to(torch.bfloat16) if epi == 2 else None
+        out = torch.empty(M, n_out, device=dev, dtype=torch.bfloat16)
+        for i in range(1 + PROFILE_REPS):
+            c = copies[i % ncopy]
+            G.gemv(x, c[0], wfmt, N, sc0=c[1] if len(c) > 1 else None, group=GROUP, gamma=gamma, eps=EPS,
+                   epilogue=epi, residual=res, out=out)
+        torch.cuda.synchronize()
+        log(f"{name}: {1 + PROFILE_REPS} launches")
+        del copies, base
+        torch.cuda.empty_cache()
+    a_cp = torch.ones(COPY_BYTES // 4, device=dev)
+    b_cp = torch.empty_like(a_cp)
+    for _ in range(3):
+        torch.mul(a_cp, 1.0, out=b_cp)
+    torch.cuda.synchronize()
+    log(f"3 copies of {COPY_BYTES} bytes")
+    return 0
 
 
 def main() -> int:
@@ -101,10 +159,11 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-step", action="store_true", help="skip the 26-layer decode step detail")
     ap.add_argument("--no-configs", action="store_true", help="skip the per-config GEMV table (C1-C4)")
-    ap.add_argument("--profile-gateup", action="store_true",
-                    help="only launch the gate|up GEMV (eagerly) and a 256 MiB copy, for counter runs")
+    ap.add_argument("--no-floors", action="store_true", help="skip the launch and streaming-read floors")
+    ap.add_argument("--profile-gemvs", action="store_true",
+                    help="only launch the PROFILE_CASES GEMVs (eagerly) and a 256 MiB copy, for counter runs")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
-                    help="summarize two rocprofv3 --pmc runs of --profile-gateup")
+                    help="summarize two rocprofv3 --pmc runs of --profile-gemvs")
     ap.add_argument("--profile-tiles", action="store_true",
                     help="only launch the several-row (C4, M = 16 and 32) GEMVs eagerly, for counter runs")
     ap.add_argument("--profile-depth", action="store_true",
@@ -138,6 +197,8 @@ def main() -> int:
     log(f"device {torch.cuda.get_device_name(0)}")
     if args.profile_tiles:
         return profile_tiles(torch, G, dev)
+    if args.profile_gemvs:
+        return profile_gemvs(torch, G, dev)
     if args.profile_depth:
         print(json.dumps({"depth_frame": depth_frame(torch, dev, log)}), flush=True)
         return 0
@@ -152,23 +213,25 @@ def main() -> int:
     gu_p, gu_sz, _ = G.quantize_int4_device(w_gu.to(dev), GROUP, True, G.W_INT4_ZP)
     dn_p, dn_sz, _ = G.quantize_int4_device(w_dn.to(dev), GROUP, True, G.W_INT4_ZP)
     del w_gu, w_dn
+    # the decode layout: gate|up tiled paired (8 gate + 8 up rows per block), down tiled
+    gu_t = G.pack_tiled(G.W_INT4_ZP, gu_p, K1, G.W_INT4_TILED_PAIRED, sc0=gu_sz)
+    dn_t = G.pack_tiled(G.W_INT4_ZP, dn_p, K2, G.W_INT4_TILED, sc0=dn_sz)
     gamma_d, x_d = gamma.to(dev), x.to(dev)
     b_gu = algo_bytes(4, N1, K1, M, True, 1)
     b_dn = algo_bytes(4, N2, K2, M, False, 0)
     step_bytes = b_gu + b_dn
-    wbytes = sum(t.numel() * t.element_size() for t in (gu_p, gu_sz, dn_p, dn_sz))
+    wbytes = gu_t.numel() + dn_t.numel()
     ncopy = max(2, -(-(1 << 30) // wbytes))
-    copies = [(gu_p.clone(), gu_sz.clone(), dn_p.clone(), dn_sz.clone()) for _ in range(ncopy)]
+    copies = [(gu_t.clone(), dn_t.clone()) for _ in range(ncopy)]
     h = torch.empty(M, N1 // 2, device=dev, dtype=torch.bfloat16)
     y = torch.empty(M, N2, device=dev, dtype=torch.bfloat16)
     log(f"C2 M={M}: {ncopy} weight copies ({ncopy * wbytes / 2**30:.2f} GiB), {step_bytes} algorithmic bytes/step")
 
     def gate_up(c):
-        G.gemv(x_d, c[0], G.W_INT4_ZP, N1, sc0=c[1], group=GROUP, gamma=gamma_d, eps=EPS,
-               epilogue=G.EPI_SILU_GATE, out=h)
+        G.gemv(x_d, c[0], G.W_INT4_TILED_PAIRED, N1, gamma=gamma_d, eps=EPS, epilogue=G.EPI_SILU_GATE, out=h)
 
     def down(c):
-        G.gemv(h, c[2], G.W_INT4_ZP, N2, sc0=c[3], group=GROUP, out=y)
+        G.gemv(h, c[1], G.W_INT4_TILED, N2, out=y)
 
     def step(i):
         c = copies[i % ncopy]
@@ -197,17 +260,6 @@ def main() -> int:
         e_ev.record()
         torch.cuda.synchronize()
         return s_ev.elapsed_time(e_ev), time.perf_counter() - t0
-
-    if args.profile_gateup:
-        for i in range(4 * ncopy):
-            gate_up(copies[i % ncopy])
-        a_cp = torch.ones(COPY_BYTES // 4, device=dev)
-        b_cp = torch.empty_like(a_cp)
-        for _ in range(3):
-            torch.mul(a_cp, 1.0, out=b_cp)
-        torch.cuda.synchronize()
-        log(f"profile run done: {4 * ncopy} gate|up launches, 3 copies of {COPY_BYTES} bytes")
-        return 0
 
     # ---- eager check of one step against a dequantize-then-matmul on the GPU
     step(0)
@@ -255,28 +307,45 @@ def main() -> int:
     traffic = read_traffic()
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                "kernel": "gemv_persist int4-zp SiLU-gate K2560 N20480 M1 (+RMSNorm)",
+                "kernel": "gemv_stream int4 tiled-paired SiLU-gate K2560 N20480 M1 (+RMSNorm)",
                 "algorithmic_bytes": b_gu, "avg_launch_us": round(us_gu, 3)}
     log(f"gate|up {us_gu:.2f} us ({achieved:.0f} GB/s), down {us_dn:.2f} us "
         f"({b_dn / us_dn / 1e3:.0f} GB/s)")
     del copies
+
+    # ---- the same two GEMVs over the row-major layout (the other kernels)
+    rm = [(gu_p.clone(), gu_sz.clone(), dn_p.clone(), dn_sz.clone()) for _ in range(ncopy)]
+    g_rm = capture(lambda i: G.gemv(x_d, rm[i % ncopy][0], G.W_INT4_ZP, N1, sc0=rm[i % ncopy][1], group=GROUP,
+                                    gamma=gamma_d, eps=EPS, epilogue=G.EPI_SILU_GATE, out=h), reps)
+    us_gu_rm = per_launch_us(g_rm)
+    del g_rm
+    g_rm = capture(lambda i: G.gemv(h, rm[i % ncopy][2], G.W_INT4_ZP, N2, sc0=rm[i % ncopy][3], group=GROUP,
+                                    out=y), reps)
+    us_dn_rm = per_launch_us(g_rm)
+    del g_rm, rm
     torch.cuda.empty_cache()
+    log(f"row-major layout: gate|up {us_gu_rm:.2f} us, down {us_dn_rm:.2f} us")
 
     detail = {
         "gate_up_us": round(us_gu, 3), "down_us": round(us_dn, 3),
         "down_gbps": round(b_dn / us_dn / 1e3, 1),
+        "rowmajor_gate_up_us": round(us_gu_rm, 3), "rowmajor_down_us": round(us_dn_rm, 3),
         "step_roofline_us": round(step_bytes / HBM_PEAK_GBPS / 1e3, 3),
         "parity_rel_err": {"gate_up": err_h, "down": err_y},
     }
+    if not args.no_floors:
+        detail["floors"] = floors(torch, G, dev, log)
 
     # ---- full synthetic decode step (26 int4 layers + bf16 head), M = 1
     if not args.no_step:
         detail["decode_step"] = decode_step(torch, G, dev, log, 1)
         detail["decode_step_m2"] = decode_step(torch, G, dev, log, 2)
+        detail["decode_step_rowmajor"] = decode_step(torch, G, dev, log, 1, layout="rowmajor")
         detail["decode_step_attn"] = decode_step(torch, G, dev, log, 2, attn_pos=1023, cache_len=1024)
         detail["depth_frame"] = depth_frame(torch, dev, log)
     if not args.no_configs:
         detail["configs"] = config_table(torch, G, dev, log)
+        detail["library_bf16_linear"] = library_table(torch, dev, log)
         detail["attention"] = attention_table(torch, dev, log)
         detail["fp32_heads"] = heads_table(torch, dev, log)
 
@@ -295,6 +364,15 @@ def main() -> int:
                          f"24 rotated weight copies",
                "us_per_step": round(r["us_per_step"], 1)}
         log(f"CPU: {r['us_per_step']:.0f} us/step on {r['threads']} threads")
+        from oracle.cpu_baseline import time_mlp_steps_predequant
+
+        r2 = time_mlp_steps_predequant(x, gamma, (gu_p.cpu(), gu_sz.cpu()), (dn_p.cpu(), dn_sz.cpu()), GROUP,
+                                       step_bytes, budget_s=args.cpu_seconds)
+        cpu["predequantized"] = {
+            "value": r2["tbps"], "unit": "TB/s", "cores": r2["threads"], "us_per_step": round(r2["us_per_step"], 1),
+            "sample": f"{r2['steps']} of the same steps with the weights dequantized to fp32 once "
+                      f"({r2['fp32_bytes_per_step']} fp32 weight bytes per step, {r2['copies']} rotated copies)"}
+        log(f"CPU, pre-dequantized fp32 weights: {r2['us_per_step']:.0f} us/step")
 
     out = {
         "metric": "int4/fp8 GEMV achieved HBM TB/s at M=1; µs per decoder-layer decode step",
@@ -311,7 +389,8 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": "int4 group-128 decoder-MLP GEMVs, M=1: RMSNorm->gate|up K2560 N2x10240 "
                                "SiLU-gate, then down K10240 N2560",
-                   "weights": "int4 symmetric g128 (bf16 scales), bf16 activations, fp32 accumulate",
+                   "weights": "int4 symmetric g128 (bf16 scales) in the 16-row tiled layout (gate|up paired), "
+                              "bf16 activations, fp32 accumulate",
                    "M": 1, "parallelism": "single GPU"},
         "roofline": roofline,
         "cpu_baseline": cpu,
@@ -408,12 +487,16 @@ def mfma_summary(trace_dir: str, pmc_dir: str) -> int:
 
 
 def pmc_summary(fetch_dir: str, write_dir: str) -> int:
-    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the gate|up GEMV from
-    two rocprofv3 counter runs of --profile-gateup, each scaled by the ratio
-    of the known bytes of the 256 MiB copy to what the counter read for it."""
+    """Per-launch FETCH_SIZE / WRITE_SIZE (KiB) of each PROFILE_CASES GEMV
+    from two rocprofv3 counter runs of --profile-gemvs, each scaled by the
+    ratio of the known bytes of the 256 MiB copy to what the counter read for
+    it; the median over each case's PROFILE_REPS launches (the warm-up
+    launch dropped)."""
     import csv
     import glob
     import statistics
+
+    n = 1 + PROFILE_REPS
 
     def load(d, counter):
         paths = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
@@ -423,31 +506,140 @@ def pmc_summary(fetch_dir: str, write_dir: str) -> int:
         for row in csv.DictReader(open(paths[0])):
             if row["Counter_Name"] != counter:
                 continue
-            key = row["Dispatch_Id"]
+            key = int(row["Dispatch_Id"])
             per.setdefault(key, [row["Kernel_Name"], 0.0])[1] += float(row["Counter_Value"])
-        gemv = [v for n, v in per.values() if "gemv_persist" in n or "gemv_mfma" in n]
-        copy = [v for n, v in per.values() if "elementwise" in n.lower() and "mul" in n.lower()]
-        if len(gemv) < 8 or not copy:
-            raise SystemExit(f"{d}: {len(gemv)} GEMV and {len(copy)} copy dispatches found")
-        return statistics.median(gemv[4:]), statistics.median(copy), len(gemv)
+        seq = [per[k] for k in sorted(per)]
+        gemv = [(name, v) for name, v in seq if "gemv_" in name]
+        copy = [v for name, v in seq if "elementwise" in name.lower() and "mul" in name.lower()]
+        if len(gemv) != n * len(PROFILE_CASES) or not copy:
+            raise SystemExit(f"{d}: {len(gemv)} GEMV dispatches (expected {n * len(PROFILE_CASES)}), "
+                             f"{len(copy)} copy dispatches")
+        cases = [gemv[i * n + 1:(i + 1) * n] for i in range(len(PROFILE_CASES))]
+        return [(c[0][0], statistics.median(v for _, v in c)) for c in cases], statistics.median(copy)
 
-    f_gemv, f_copy, n_f = load(fetch_dir, "FETCH_SIZE")
-    w_gemv, w_copy, n_w = load(write_dir, "WRITE_SIZE")
+    fetch, f_copy = load(fetch_dir, "FETCH_SIZE")
+    write, w_copy = load(write_dir, "WRITE_SIZE")
     kib = COPY_BYTES / 1024
     fr, wr = kib / f_copy, kib / w_copy
-    traffic = int(round((f_gemv * fr + w_gemv * wr) * 1024))
-    b_gu = algo_bytes(4, 20480, 2560, 1, True, 1)
-    print(f"kernel: gemv int4-zp SiLU-gate K2560 N20480 M1 (+RMSNorm), median of {n_f - 4} / {n_w - 4} dispatches")
-    print(f"FETCH_SIZE per launch (KiB, raw): {f_gemv:.1f}")
-    print(f"WRITE_SIZE per launch (KiB, raw): {w_gemv:.1f}")
-    print(f"copy kernel {COPY_BYTES} B: FETCH_SIZE {f_copy:.1f} KiB -> read scale {fr:.4f}; "
+    print(f"HBM traffic per launch, median of {PROFILE_REPS} launches per case; counters scaled by a "
+          f"{COPY_BYTES}-byte copy: FETCH_SIZE {f_copy:.1f} KiB -> read scale {fr:.4f}, "
           f"WRITE_SIZE {w_copy:.1f} KiB -> write scale {wr:.4f}")
-    print(f"fetch_bytes_per_launch: {int(round(f_gemv * fr * 1024))}")
-    print(f"write_bytes_per_launch: {int(round(w_gemv * wr * 1024))}")
-    print(f"traffic_bytes_per_launch: {traffic}")
-    print(f"algorithmic_bytes_per_launch: {b_gu}")
-    print(f"traffic / algorithmic: {traffic / b_gu:.4f}")
+    print(f"{'case':52s} {'algorithmic B':>13s} {'fetch B':>11s} {'write B':>9s} {'traffic B':>11s} "
+          f"{'traffic/algo':>12s}  kernel")
+    lines = []
+    for case, (kname, f), (_, w) in zip(PROFILE_CASES, fetch, write):
+        name, fmt, layout, N, K, M, epi, norm = case
+        algo = algo_bytes(4 if fmt == "int4" else 8, N, K, M, norm, epi)
+        fb, wb = int(round(f * fr * 1024)), int(round(w * wr * 1024))
+        kern = re.search(r"gemv_\w+<[^>]*>", kname)
+        print(f"{name:52s} {algo:13d} {fb:11d} {wb:9d} {fb + wb:11d} {(fb + wb) / algo:12.4f}  "
+              f"{kern.group(0) if kern else kname[:60]}")
+        lines.append(f"traffic_bytes_per_launch[{name}]: {fb + wb}")
+    for line in lines:
+        print(line)
     return 0
+
+
+FLOOR_MIB = (13, 26, 52)
+
+
+def floors(torch, G, dev, log) -> dict:
+    """What any launch costs and what streaming can reach on this GPU, as
+    HIP-graph replays:
+      empty_node_us  one empty workgroup (bz_stream_read with no bytes),
+                     launched back to back in a graph;
+      read           bz_stream_read (non-temporal 16-byte loads, nothing
+                     written) over 13, 26 and 52 MiB -- the sizes of the int4
+                     down, int4 gate|up and fp8 gate|up weights -- rotating
+                     through >= 1 GiB, with the line t = fixed + bytes / rate
+                     fitted through the three points;
+      copy_1gib      torch's device-to-device copy of 1 GiB (read + write)."""
+    from breeze_amd.fused.kernels import graph_time_us
+
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    empty = graph_time_us(lambda: G.stream_read(None, sink), iters=256)
+    reads = []
+    for mib in FLOOR_MIB:
+        size = mib << 20
+        ncopy = max(2, -(-(1 << 30) // size))
+        pool = torch.randint(0, 1 << 30, (ncopy * size // 4,), dtype=torch.int32, device=dev)
+        bufs = [pool[i * size // 4:(i + 1) * size // 4] for i in range(ncopy)]
+        st = {"i": 0}
+
+        def fn():
+            G.stream_read(bufs[st["i"] % ncopy], sink)
+            st["i"] += 1
+
+        us = graph_time_us(fn, iters=min(2 * ncopy, 256))
+        reads.append({"mib": mib, "bytes": size, "us": round(us, 3), "gbps": round(size / us / 1e3, 1)})
+        log(f"read floor {mib} MiB: {us:.2f} us ({size / us / 1e3:.0f} GB/s)")
+        del pool, bufs
+    xs = [r["bytes"] for r in reads]
+    ys = [r["us"] for r in reads]
+    xm, ym = sum(xs) / len(xs), sum(ys) / len(ys)
+    slope = sum((a - xm) * (b - ym) for a, b in zip(xs, ys)) / sum((a - xm) ** 2 for a in xs)
+    fixed = ym - slope * xm
+    a = torch.empty(1 << 28, dtype=torch.int32, device=dev)
+    b = torch.empty_like(a)
+    a.fill_(1)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_ev.record()
+    for _ in range(5):
+        b.copy_(a)
+    e_ev.record()
+    torch.cuda.synchronize()
+    copy_us = s_ev.elapsed_time(e_ev) * 1e3 / 5
+    del a, b
+    torch.cuda.empty_cache()
+    log(f"empty node {empty:.2f} us; read line {fixed:.2f} us + bytes at {1 / slope / 1e3:.0f} GB/s; "
+        f"1 GiB copy {copy_us:.0f} us ({2 * (1 << 30) / copy_us / 1e3:.0f} GB/s read+write)")
+    return {"empty_node_us": round(empty, 3), "read": reads,
+            "read_fit": {"fixed_us": round(fixed, 3), "gbps": round(1 / slope / 1e3, 1)},
+            "copy_1gib": {"us": round(copy_us, 1), "gbps_read_plus_write": round(2 * (1 << 30) / copy_us / 1e3, 1)}}
+
+
+# The library comparator of the reference (bench_gemv.py:36-42): cuBLAS bf16
+# F.linear on cold weight copies; here torch's bf16 linear (hipBLASLt).
+LIBRARY_SHAPES = [
+    ("gate|up K2560 N20480", 20480, 2560),
+    ("down K10240 N2560", 2560, 10240),
+    ("qkv K2560 N4096", 4096, 2560),
+    ("o_proj K4096 N2560", 2560, 4096),
+]
+
+
+def library_table(torch, dev, log) -> list:
+    """bf16 torch.nn.functional.linear (hipBLASLt) at the C2/C3 GEMV shapes,
+    M = 1 and 2, weights N(0, 0.02) in bf16 rotating through >= 1 GiB, timed
+    as graph replays.  Roofline bytes: bf16 weights + x + output."""
+    from breeze_amd.fused.kernels import graph_time_us
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    rows = []
+    for name, N, K in LIBRARY_SHAPES:
+        w = (torch.randn(N, K, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+        ncopy = max(2, -(-(1 << 30) // (2 * N * K)))
+        ws = [w.clone() for _ in range(ncopy)]
+        for M in (1, 2):
+            x = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
+            st = {"i": 0}
+
+            def fn():
+                torch.nn.functional.linear(x, ws[st["i"] % ncopy])
+                st["i"] += 1
+
+            us = graph_time_us(fn, iters=min(2 * ncopy, 128))
+            nbytes = 2 * N * K + 2 * M * K + 2 * M * N
+            roof = nbytes / HBM_PEAK_GBPS / 1e3
+            rows.append({"shape": name, "M": M, "us": round(us, 2), "gbps": round(nbytes / us / 1e3, 1),
+                         "roofline_us": round(roof, 2), "frac": round(roof / us, 3)})
+            log(f"bf16 F.linear {name} M={M}: {us:6.2f} us ({nbytes / us / 1e3:5.0f} GB/s)")
+        del ws, w
+        torch.cuda.empty_cache()
+    return rows
 
 
 # (name, weight format, N, K, epilogue, RMSNorm prologue, M values): the
@@ -471,11 +663,30 @@ CONFIG_SHAPES = [
 ]
 
 
+def _weights(torch, G, fmt, N, K, epi, w, layout):
+    """(buffers, format, bits, gemv kwargs) of a synthetic weight in the
+    tiled decode layout (paired for SiLU-gate) or the row-major one."""
+    if fmt == "int4":
+        p, sz, _ = G.quantize_int4_device(w, GROUP, True, G.W_INT4_ZP)
+        if layout == "tiled":
+            wfmt = G.W_INT4_TILED_PAIRED if epi == 1 else G.W_INT4_TILED
+            return (G.pack_tiled(G.W_INT4_ZP, p, K, wfmt, sc0=sz),), wfmt, 4
+        return (p, sz), G.W_INT4_ZP, 4
+    c, sc = G.quantize_fp8_device(w, 1e-12)
+    if layout == "tiled":
+        wfmt = G.W_FP8_TILED_PAIRED if epi == 1 else G.W_FP8_TILED
+        return (G.pack_tiled(G.W_FP8, c.view(torch.uint8), K, wfmt, sc0=sc),), wfmt, 8
+    return (c.view(torch.uint8), sc), G.W_FP8, 8
+
+
 def config_table(torch, G, dev, log) -> list:
     """Each GEMV of C1-C4 (synthetic weights N(0, 0.02), int4 symmetric g128
-    or fp8 e4m3 per-row, bf16 x N(0, 1)), timed as HIP-graph replays over
-    weight copies rotating through >= 1 GiB: µs per call, algorithmic GB/s
-    and the fraction of the 8 TB/s bytes-moved roofline."""
+    or fp8 e4m3 per-row, bf16 x N(0, 1)) in both layouts -- "tiled" (the
+    decode layout the modules hold, streaming kernel, slices of <= 8 rows)
+    and "rowmajor" (the other kernels: row-sliced paths, and the several-row
+    tile kernel from M = 5) -- timed as HIP-graph replays over weight copies
+    rotating through >= 1 GiB: µs per call, algorithmic GB/s and the fraction
+    of the 8 TB/s bytes-moved roofline."""
     from breeze_amd import tuning
     from breeze_amd.fused.kernels import graph_time_us
 
@@ -484,43 +695,41 @@ def config_table(torch, G, dev, log) -> list:
     rows = []
     for name, fmt, N, K, epi, norm, Ms in CONFIG_SHAPES:
         w = torch.randn(N, K, device=dev, generator=gen) * 0.02
-        if fmt == "int4":
-            p, sz, _ = G.quantize_int4_device(w, GROUP, True, G.W_INT4_ZP)
-            base = (p, sz)
-            wfmt, bits = G.W_INT4_ZP, 4
-        else:
-            c, sc = G.quantize_fp8_device(w, 1e-12)
-            base = (c.view(torch.uint8), sc)
-            wfmt, bits = G.W_FP8, 8
-        del w
-        wbytes = sum(t.numel() * t.element_size() for t in base)
-        ncopy = max(2, -(-(1 << 30) // wbytes))
-        copies = [tuple(t.clone() for t in base) for _ in range(ncopy)]
         gamma = (1 + 0.1 * torch.randn(K, device=dev, generator=gen)).to(torch.bfloat16) if norm else None
+        xs = {M: torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16) for M in Ms}
         n_out = N // 2 if epi == 1 else N
-        for M in Ms:
-            x = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
-            out = torch.empty(M, n_out, device=dev, dtype=torch.bfloat16)
-            st = {"i": 0}
+        for layout in ("tiled", "rowmajor"):
+            base, wfmt, bits = _weights(torch, G, fmt, N, K, epi, w, layout)
+            wbytes = sum(t.numel() * t.element_size() for t in base)
+            ncopy = max(2, -(-(1 << 30) // wbytes))
+            copies = [tuple(t.clone() for t in base) for _ in range(ncopy)]
+            del base
+            for M in Ms:
+                x = xs[M]
+                out = torch.empty(M, n_out, device=dev, dtype=torch.bfloat16)
+                st = {"i": 0}
 
-            def call():
-                c = copies[st["i"] % ncopy]
-                st["i"] += 1
-                G.gemv(x, c[0], wfmt, N, sc0=c[1], group=GROUP, gamma=gamma, eps=EPS, epilogue=epi, out=out)
+                def call():
+                    c = copies[st["i"] % ncopy]
+                    st["i"] += 1
+                    sc = c[1] if len(c) > 1 else None
+                    G.gemv(x, c[0], wfmt, N, sc0=sc, group=GROUP, gamma=gamma, eps=EPS, epilogue=epi, out=out)
 
-            us = graph_time_us(call, iters=2 * ncopy)
-            nbytes = algo_bytes(bits, N, K, M, norm, epi)
-            roof = nbytes / HBM_PEAK_GBPS / 1e3
-            tflops = 2.0 * M * N * K / us / 1e6
-            launch = tuning.lookup(dev, N, K, wfmt, epi, norm, M)
-            rows.append({"config": name, "M": M, "us": round(us, 2), "gbps": round(nbytes / us / 1e3, 1),
-                         "roofline_us": round(roof, 2), "frac": round(roof / us, 3),
-                         "tflops": round(tflops, 2), "mfma_peak_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 5),
-                         "launch": list(launch) if launch else "rule"})
-            log(f"{name:42s} M={M:2d}: {us:7.2f} us  {nbytes / us / 1e3:6.0f} GB/s  "
-                f"({roof / us * 100:4.1f}% of roofline)")
-        del copies
-        torch.cuda.empty_cache()
+                us = graph_time_us(call, iters=2 * ncopy)
+                nbytes = algo_bytes(bits, N, K, M, norm, epi)
+                roof = nbytes / HBM_PEAK_GBPS / 1e3
+                tflops = 2.0 * M * N * K / us / 1e6
+                launch = tuning.lookup(dev, N, K, wfmt, epi, norm, M) if layout == "rowmajor" else None
+                rows.append({"config": name, "layout": layout, "M": M, "us": round(us, 2),
+                             "gbps": round(nbytes / us / 1e3, 1), "roofline_us": round(roof, 2),
+                             "frac": round(roof / us, 3), "tflops": round(tflops, 2),
+                             "mfma_peak_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 5),
+                             "launch": list(launch) if launch else "rule"})
+                log(f"{name:42s} {layout:8s} M={M:2d}: {us:7.2f} us  {nbytes / us / 1e3:6.0f} GB/s  "
+                    f"({roof / us * 100:4.1f}% of roofline)")
+            del copies
+            torch.cuda.empty_cache()
+        del w
     return rows
 
 
@@ -619,31 +828,46 @@ def heads_table(torch, dev, log) -> list:
     return rows
 
 
-def decode_step(torch, G, dev, log, M: int = 1, attn_pos: int | None = None, cache_len: int = 1024) -> dict:
+def decode_step(torch, G, dev, log, M: int = 1, attn_pos: int | None = None, cache_len: int = 1024,
+                layout: str = "tiled") -> dict:
     """26 decoder layers (hidden 2560, 16x256 q heads, 4 KV heads, MLP 10240)
     of int4 group-128 weights: RMSNorm->QKV, attention replaced by a copy of
-    [M, 4096], o_proj + residual, RMSNorm->gate|up SiLU-gate, down + residual;
-    then a final RMSNorm -> bf16 head K2560 N8192.  One HIP graph per step.
+    the [M, 4096] query part, o_proj + residual, RMSNorm->gate|up SiLU-gate,
+    down + residual; then a final RMSNorm -> bf16 head K2560 N8192.  One HIP
+    graph per step.
+
+    layout "tiled" (the decode layout): the QKV GEMV stores its first 4096
+    columns a second time into the attention-output buffer (the copy, done
+    by the same launch), and the first layer reads the step's input directly,
+    so the graph holds GEMV launches only.  layout "rowmajor": the row-major
+    kernels, the copy as a device copy node.
 
     With ``attn_pos`` the copy is replaced by the real decode attention step
     (q/k RMSNorm + RoPE + cache write, attention over cache positions
     [0, attn_pos] of a bf16 cache of ``cache_len`` positions per layer); its
-    algorithmic bytes (keys and values read once) join the roofline."""
+    algorithmic bytes (keys and values read once) join the roofline.
+
+    Returns µs per step against the bytes-moved roofline, and a checksum of
+    the logits (float64 sum) for comparison across layouts and runs."""
     H, QKV, ATT, MLP, LAYERS, VOCAB = 2560, 6144, 4096, 10240, 26, 8192
     HQ, HKV, D = 16, 4, 256
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
+    tiled = layout == "tiled"
 
-    def q4(n, k):
+    def q4(n, k, paired=False):
         w = torch.randn(n, k, device=dev, generator=gen) * 0.02
         p, sz, _ = G.quantize_int4_device(w, GROUP, True, G.W_INT4_ZP)
-        return p, sz
+        if not tiled:
+            return {"w": p, "sc0": sz, "wfmt": G.W_INT4_ZP, "group": GROUP}
+        wfmt = G.W_INT4_TILED_PAIRED if paired else G.W_INT4_TILED
+        return {"w": G.pack_tiled(G.W_INT4_ZP, p, k, wfmt, sc0=sz), "wfmt": wfmt}
 
     def gam(k):
         return (1 + 0.1 * torch.randn(k, device=dev, generator=gen)).to(torch.bfloat16)
 
-    layers = [dict(qkv=q4(QKV, H), o=q4(H, ATT), gu=q4(2 * MLP, H), dn=q4(H, MLP), g1=gam(H), g2=gam(H))
-              for _ in range(LAYERS)]
+    layers = [dict(qkv=q4(QKV, H), o=q4(H, ATT), gu=q4(2 * MLP, H, paired=True), dn=q4(H, MLP), g1=gam(H),
+                   g2=gam(H)) for _ in range(LAYERS)]
     head = (torch.randn(VOCAB, H, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
     gf = gam(H)
     h0 = torch.randn(M, H, device=dev, generator=gen).to(torch.bfloat16)
@@ -666,20 +890,24 @@ def decode_step(torch, G, dev, log, M: int = 1, attn_pos: int | None = None, cac
         mask = torch.zeros(M, 1, 1, cache_len, device=dev, dtype=torch.bfloat16)
         split = AT.default_split(cache_len)
 
+    def gemv(x, wt, n, **kw):
+        G.gemv(x, n=n, **wt, **kw)
+
     def run():
-        hs.copy_(h0)
-        for L in layers:
-            G.gemv(hs, L["qkv"][0], G.W_INT4_ZP, QKV, sc0=L["qkv"][1], group=GROUP, gamma=L["g1"], eps=EPS, out=qkv)
+        if not tiled:
+            hs.copy_(h0)
+        for i, L in enumerate(layers):
+            x_in = h0 if (tiled and i == 0) else hs
+            second = {"out2": att} if (tiled and attn_pos is None) else {}
+            gemv(x_in, L["qkv"], QKV, gamma=L["g1"], eps=EPS, out=qkv, **second)
             if attn_pos is None:
-                att.copy_(qkv[:, :ATT])
+                if not tiled:
+                    att.copy_(qkv[:, :ATT])
             else:
                 AT.attention_step(qkv, cos, sin, pos, L["k"], L["v"], mask, L["qn"], L["kn"], EPS, att, split=split)
-            G.gemv(att, L["o"][0], G.W_INT4_ZP, H, sc0=L["o"][1], group=GROUP, epilogue=G.EPI_RESIDUAL,
-                   residual=hs, out=hs)
-            G.gemv(hs, L["gu"][0], G.W_INT4_ZP, 2 * MLP, sc0=L["gu"][1], group=GROUP, gamma=L["g2"], eps=EPS,
-                   epilogue=G.EPI_SILU_GATE, out=mid)
-            G.gemv(mid, L["dn"][0], G.W_INT4_ZP, H, sc0=L["dn"][1], group=GROUP, epilogue=G.EPI_RESIDUAL,
-                   residual=hs, out=hs)
+            gemv(att, L["o"], H, epilogue=G.EPI_RESIDUAL, residual=x_in, out=hs)
+            gemv(hs, L["gu"], 2 * MLP, gamma=L["g2"], eps=EPS, epilogue=G.EPI_SILU_GATE, out=mid)
+            gemv(mid, L["dn"], H, epilogue=G.EPI_RESIDUAL, residual=hs, out=hs)
         G.gemv(hs, head, G.W_BF16, VOCAB, gamma=gf, eps=EPS, out=logits)
 
     mid_bytes = 2 * 2 * M * ATT  # the copy: read and write [M, 4096] bf16
@@ -693,6 +921,7 @@ def decode_step(torch, G, dev, log, M: int = 1, attn_pos: int | None = None, cac
         + algo_bytes(16, VOCAB, H, M, True, 0)
     run()
     torch.cuda.synchronize()
+    checksum = float(logits.double().sum().item())
     st = torch.cuda.Stream()
     st.wait_stream(torch.cuda.current_stream())
     g = torch.cuda.CUDAGraph()
@@ -703,6 +932,7 @@ def decode_step(torch, G, dev, log, M: int = 1, attn_pos: int | None = None, cac
     for _ in range(3):
         g.replay()
     torch.cuda.synchronize()
+    replay_checksum = float(logits.double().sum().item())
     reps = 20
     s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s_ev.record()
@@ -713,11 +943,13 @@ def decode_step(torch, G, dev, log, M: int = 1, attn_pos: int | None = None, cac
     us = s_ev.elapsed_time(e_ev) * 1e3 / reps
     roof = nbytes / HBM_PEAK_GBPS / 1e3
     what = "copy for attention" if attn_pos is None else f"attention at position {attn_pos} of {cache_len}"
-    log(f"decode step (26 layers + head, M={M}, {what}): {us:.1f} us, roofline {roof:.1f} us ({us / roof:.2f}x)")
+    log(f"decode step ({layout}, 26 layers + head, M={M}, {what}): {us:.1f} us, roofline {roof:.1f} us "
+        f"({us / roof:.2f}x), logits checksum {checksum:.6e}")
     del g, layers, head
     torch.cuda.empty_cache()
     res = {"us": round(us, 2), "algorithmic_bytes": nbytes, "roofline_us": round(roof, 2),
-           "x_roofline": round(us / roof, 3), "M": M}
+           "x_roofline": round(us / roof, 3), "M": M, "layout": layout, "logits_checksum": checksum,
+           "replay_matches_eager": replay_checksum == checksum}
     if attn_pos is not None:
         res.update(attn_pos=attn_pos, cache_len=cache_len)
     return res

@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede loading the HIP library)
 
 LIB_PATH = Path(os.environ.get("BZ_LIB", str(Path(__file__).resolve().parent / "libbzgemv.so")))
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # enums of include/bz_gemv.h
 OK = 0
@@ -48,6 +48,7 @@ EXPORTS = (
     "bz_attn_workspace",
     "bz_attn_default_split",
     "bz_sample_cfg",
+    "bz_stream_read",
 )
 
 
@@ -80,6 +81,10 @@ class GemvDesc(ctypes.Structure):
         ("ldo", ctypes.c_int64),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
+        ("out2", ctypes.c_void_p),
+        ("ldo2", ctypes.c_int64),
+        ("n_out2", ctypes.c_int32),
+        ("reserved0", ctypes.c_int32),
     ]
 
 
@@ -133,6 +138,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.bz_attn_workspace.argtypes = [i32, i32, i32, i32, i32]
     lib.bz_attn_default_split.restype = ctypes.c_int32
     lib.bz_attn_default_split.argtypes = [i32]
+    lib.bz_stream_read.restype = ctypes.c_int
+    lib.bz_stream_read.argtypes = [vp, ctypes.c_size_t, ctypes.c_uint32, vp, vp]
     lib.bz_sample_cfg.restype = ctypes.c_int
     lib.bz_sample_cfg.argtypes = [vp, i64, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
 

@@ -103,8 +103,12 @@ def gemv(
     out: Optional[torch.Tensor] = None,
     out_dtype: torch.dtype = torch.bfloat16,
     cfg: tuple = (0, 0, 0, 0, 0),
+    out2: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """out[M, N_out] = epilogue(rmsnorm?(x) @ w_eff^T) in one launch.
+
+    ``out2`` [M, n2] (tiled formats only, out's dtype, n2 <= N_out): columns
+    [0, n2) of the result are stored there as well, by the same launch.
 
     ``cfg`` (depth, waves, tiles, path[, slices]) all zero takes the static
     per-arch table's launch shape for this GEMV if it has one (tuning.py),
@@ -145,6 +149,11 @@ def gemv(
         _require_gpu("out", out, dev)
         if out.dtype not in _DT or out.shape != (M, n_out) or out.stride(1) != 1:
             raise ValueError("out must be a bf16/fp32 [M, N_out] row-major tensor")
+    if out2 is not None:
+        _require_gpu("out2", out2, dev)
+        if out2.dim() != 2 or out2.dtype != out.dtype or out2.shape[0] != M or out2.stride(1) != 1 \
+                or not 0 < out2.shape[1] <= n_out:
+            raise ValueError(f"out2 must be a row-major [M, <= {n_out}] tensor of out's dtype")
     for name, t in (("sc0", sc0), ("sc1", sc1)):
         if t is not None:
             _require_gpu(name, t, dev)
@@ -174,6 +183,8 @@ def gemv(
     if epilogue == EPI_RESIDUAL:
         d.residual, d.ldr = residual.data_ptr(), residual.stride(0)
     d.out, d.ldo = out.data_ptr(), out.stride(0)
+    if out2 is not None:
+        d.out2, d.ldo2, d.n_out2 = out2.data_ptr(), out2.stride(0), out2.shape[1]
     if M >= _TILE_MIN_ROWS or cfg[3] == _PATH_TILE:
         need = _lib.lib().bz_gemv_workspace(ctypes.byref(d))
         if need:
@@ -346,6 +357,18 @@ def gemv_traceable(x, w, wfmt, n, *, sc0=None, sc1=None, group=128, gamma=None, 
         )
     return gemv(x, w, wfmt, n, sc0=sc0, sc1=sc1, group=group, gamma=gamma, eps=eps,
                 epilogue=epilogue, residual=residual, out_dtype=out_dtype)
+
+
+def stream_read(buf: Optional[torch.Tensor], sink: torch.Tensor, key: int = 0x9E3779B9) -> None:
+    """Launch the read-floor kernel over ``buf`` (bytes a multiple of 16 KiB;
+    None: one empty workgroup).  ``sink`` is an int32 device tensor, written
+    only if a thread's XOR of its data equals ``key``."""
+    _require_gpu("sink", sink, sink.device)
+    nbytes = 0 if buf is None else buf.numel() * buf.element_size()
+    if buf is not None and not buf.is_contiguous():
+        raise ValueError("buf must be contiguous")
+    _lib.check(_lib.lib().bz_stream_read(_ptr(buf), nbytes, key, sink.data_ptr(), _lib.stream_of(sink)),
+               "bz_stream_read")
 
 
 # ---- glue kernels ------------------------------------------------------------

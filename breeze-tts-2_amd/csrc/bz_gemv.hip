@@ -57,6 +57,8 @@ static int check_desc(const bz_gemv_desc* d, DescInfo& di) {
     if (d->out_dtype != BZ_DT_BF16 && d->out_dtype != BZ_DT_F32) return BZ_ERR_INVALID_ARG;
     if (!d->x || !d->w || !d->out) return BZ_ERR_INVALID_ARG;
     if (d->cfg_path < 0 || d->cfg_path > PATH_STREAM || d->cfg_slices < 0) return BZ_ERR_INVALID_ARG;
+    if (d->reserved0) return BZ_ERR_INVALID_ARG;
+    if (d->n_out2 && !is_tiled(wf)) return BZ_ERR_UNSUPPORTED;  // the second store is a streaming-path feature
     if (is_tiled(wf)) {
         // tiled formats: scales inside w; 16-row blocks; paired <=> SiLU-gate
         if (epi == BZ_EPI_RESIDUAL) {
@@ -69,9 +71,12 @@ static int check_desc(const bz_gemv_desc* d, DescInfo& di) {
         const int n_out = epi == BZ_EPI_SILU_GATE ? N / 2 : N;
         if (d->ldx < K || d->ldo < n_out) return BZ_ERR_INVALID_ARG;
         if (epi == BZ_EPI_RESIDUAL && d->ldr < n_out) return BZ_ERR_INVALID_ARG;
+        if (d->n_out2 < 0 || d->n_out2 > n_out || (d->n_out2 && (!d->out2 || d->ldo2 < d->n_out2)))
+            return BZ_ERR_INVALID_ARG;
         if (!aligned(d->x, 16) || (d->ldx % 8) || !aligned(d->w, 16)) return BZ_ERR_ALIGNMENT;
         if (d->gamma && !aligned(d->gamma, 16)) return BZ_ERR_ALIGNMENT;
         if (!aligned(d->out, d->out_dtype == BZ_DT_F32 ? 4 : 2)) return BZ_ERR_ALIGNMENT;
+        if (d->n_out2 && !aligned(d->out2, d->out_dtype == BZ_DT_F32 ? 4 : 2)) return BZ_ERR_ALIGNMENT;
         di.n_out = n_out;
         di.glog2 = 7;
         di.row_bytes = tiled_i4(wf) ? K / 2 : K;
@@ -248,6 +253,8 @@ static int gemv_tiled(const bz_gemv_desc* d, const DescInfo& di, hipStream_t st)
     p.gamma = static_cast<const uint16_t*>(d->gamma);
     p.ldr = d->ldr;
     p.ldo = d->ldo;
+    p.ldo2 = d->ldo2;
+    p.n_out2 = d->n_out2;
     p.eps = d->eps;
     p.K = d->K;
     p.NU = tiled_units(d->wfmt, d->K);
@@ -263,6 +270,7 @@ static int gemv_tiled(const bz_gemv_desc* d, const DescInfo& di, hipStream_t st)
         p.M = r;
         p.x = static_cast<const uint16_t*>(d->x) + (int64_t)m0 * d->ldx;
         p.out = static_cast<uint8_t*>(d->out) + (int64_t)m0 * d->ldo * osz;
+        p.out2 = d->n_out2 ? static_cast<uint8_t*>(d->out2) + (int64_t)m0 * d->ldo2 * osz : nullptr;
         p.res = d->residual ? static_cast<const uint8_t*>(d->residual) + (int64_t)m0 * d->ldr * rsz : nullptr;
         const int lrc = launch_stream(d->wfmt, p, q, st);
         if (lrc != BZ_OK) return lrc;

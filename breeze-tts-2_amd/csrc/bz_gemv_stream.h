@@ -94,6 +94,9 @@ struct StreamParams {
     int64_t ldr;
     void* out;
     int64_t ldo;
+    void* out2;     // columns [0, n_out2) stored here as well (n_out2 = 0: none)
+    int64_t ldo2;
+    int n_out2;
     float eps;
     int M, K, NU, n_out;
     int epi, out_f32, res_f32, norm;
@@ -392,11 +395,19 @@ __global__ void __launch_bounds__(1024) gemv_stream(StreamParams p) {
                     o += __uint_as_float(p.res_f32 ? rv : rv << 16);
                 }
             }
-            const int64_t oi = (int64_t)m * p.ldo + b * ocols + c;
+            const int col = b * ocols + c;
+            const int64_t oi = (int64_t)m * p.ldo + col;
             if (p.out_f32)
                 reinterpret_cast<float*>(p.out)[oi] = o;
             else
                 reinterpret_cast<uint16_t*>(p.out)[oi] = f32_to_bf16(o);
+            if (col < p.n_out2) {
+                const int64_t oi2 = (int64_t)m * p.ldo2 + col;
+                if (p.out_f32)
+                    reinterpret_cast<float*>(p.out2)[oi2] = o;
+                else
+                    reinterpret_cast<uint16_t*>(p.out2)[oi2] = f32_to_bf16(o);
+            }
         }
     }
 }

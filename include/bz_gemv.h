@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define BZ_ABI_VERSION 3
+#define BZ_ABI_VERSION 4
 
 typedef enum bz_status {
     BZ_OK = 0,
@@ -156,6 +156,12 @@ typedef struct bz_gemv_desc {
     const void* residual; int64_t ldr;
     void* out; int64_t ldo;
     void* workspace; size_t workspace_bytes;  /* path 4 split-K partials + counters */
+    /* Second store (tiled formats only): output columns [0, n_out2) are also
+     * written to out2 (same dtype as out, leading dimension ldo2), e.g. the
+     * query part of a QKV projection into the buffer of the next kernel.
+     * n_out2 = 0 disables it. */
+    void* out2; int64_t ldo2;
+    int32_t n_out2; int32_t reserved0;  /* reserved0 must be 0 */
 } bz_gemv_desc;
 
 /* ABI version of the loaded library (BZ_ABI_VERSION it was built with). */
@@ -180,6 +186,13 @@ size_t bz_gemv_workspace(const bz_gemv_desc* d);
  * Any M >= 1 is accepted (the reference fused kernel stops at M <= 2,
  * models/fused/kernels.py:336). */
 int bz_gemv(const bz_gemv_desc* d, void* stream);
+
+/* Measurement aid, no counterpart in the reference: reads `bytes` (a
+ * multiple of 16 KiB, 16-byte aligned) from device memory `p` once and
+ * writes nothing unless the XOR a thread read equals `key` (then `*sink`).
+ * Its duration is the streaming-read floor the GEMVs are compared with;
+ * bytes = 0 launches one empty workgroup (the fixed cost of a launch). */
+int bz_stream_read(const void* p, size_t bytes, uint32_t key, uint32_t* sink, void* stream);
 
 /* Size of bz_gemv_noalloc's static device workspace, per GPU. */
 #define BZ_GEMV_SCRATCH_BYTES ((size_t)8 << 20)

@@ -97,3 +97,44 @@ def time_mlp_steps(x, gamma, gu, down, group: int, algo_bytes: int, budget_s: fl
     us = el / steps * 1e6
     return {"us_per_step": us, "tbps": algo_bytes / (us * 1e-6) / 1e12, "steps": steps, "threads": threads,
             "cpu": cpu_model(), "seconds": el}
+
+
+def time_mlp_steps_predequant(x, gamma, gu, down, group: int, algo_bytes: int, budget_s: float = 10.0,
+                              min_rotation_bytes: int = 2 << 30, max_steps: int = 1000) -> dict:
+    """The same step with the weights dequantized to fp32 once, before the
+    timed loop (the bandwidth-bound CPU ceiling the reference computes in
+    bench_cpu_bound.py:24-46, which streams plain float weights over rotated
+    copies).  Copies are added until the rotation spans ``min_rotation_bytes``
+    (2 GiB by default, beyond any host last-level cache)."""
+    threads = host_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        wg = dequant_zp(gu[0], gu[1], group)
+        wd = dequant_zp(down[0], down[1], group)
+        per = (wg.numel() + wd.numel()) * 4
+        copies = max(2, -(-min_rotation_bytes // per))
+        reps = [(wg.clone(), wd.clone()) for _ in range(copies)]
+        del wg, wd
+
+        def step(g, d):
+            xn = rmsnorm_f32(x, gamma, 1e-6)
+            a = xn @ g.t()
+            half = a.shape[1] // 2
+            h = torch.nn.functional.silu(a[:, :half]) * a[:, half:]
+            return (h @ d.t()).to(torch.bfloat16)
+
+        step(*reps[0])  # warm-up
+        steps = 0
+        t0 = time.perf_counter()
+        while True:
+            step(*reps[steps % copies])
+            steps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or steps >= max_steps:
+                break
+    finally:
+        torch.set_num_threads(prev)
+    us = el / steps * 1e6
+    return {"us_per_step": us, "tbps": algo_bytes / (us * 1e-6) / 1e12, "steps": steps, "threads": threads,
+            "cpu": cpu_model(), "seconds": el, "copies": copies, "fp32_bytes_per_step": per}

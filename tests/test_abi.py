@@ -120,6 +120,13 @@ def _desc(L, **kw):
         ({"wfmt": 4, "cfg_path": 2}, "ERR_UNSUPPORTED"),       # tiled formats run path 5 only
         ({"cfg_path": 5}, "ERR_UNSUPPORTED"),                  # path 5 reads tiled formats only
         ({"cfg_path": 6}, "ERR_INVALID_ARG"),
+        ({"reserved0": 1}, "ERR_INVALID_ARG"),
+        ({"n_out2": 8, "out2": 1 << 20, "ldo2": 8}, "ERR_UNSUPPORTED"),            # second store: tiled only
+        ({"wfmt": 4, "n_out2": 8, "ldo2": 8}, "ERR_INVALID_ARG"),                # ... needs out2
+        ({"wfmt": 4, "n_out2": 65, "out2": 1 << 20, "ldo2": 65}, "ERR_INVALID_ARG"),  # ... at most N_out
+        ({"wfmt": 4, "n_out2": 8, "out2": 1 << 20, "ldo2": 4}, "ERR_INVALID_ARG"),   # ... ldo2 >= n_out2
+        ({"wfmt": 4, "n_out2": -1}, "ERR_INVALID_ARG"),
+        ({"wfmt": 4, "n_out2": 8, "out2": (1 << 20) + 1, "ldo2": 8}, "ERR_ALIGNMENT"),
         ({"wfmt": 4, "w": (1 << 20) + 8}, "ERR_ALIGNMENT"),
         ({"epilogue": 5}, "ERR_INVALID_ARG"),
         ({"out_dtype": 3}, "ERR_INVALID_ARG"),
@@ -213,6 +220,13 @@ def test_workspace_sizes(L):
     "kw,status",
     [
         ({"cfg_path": 6}, "ERR_INVALID_ARG"),
+        ({"reserved0": 1}, "ERR_INVALID_ARG"),
+        ({"n_out2": 8, "out2": 1 << 20, "ldo2": 8}, "ERR_UNSUPPORTED"),            # second store: tiled only
+        ({"wfmt": 4, "n_out2": 8, "ldo2": 8}, "ERR_INVALID_ARG"),                # ... needs out2
+        ({"wfmt": 4, "n_out2": 65, "out2": 1 << 20, "ldo2": 65}, "ERR_INVALID_ARG"),  # ... at most N_out
+        ({"wfmt": 4, "n_out2": 8, "out2": 1 << 20, "ldo2": 4}, "ERR_INVALID_ARG"),   # ... ldo2 >= n_out2
+        ({"wfmt": 4, "n_out2": -1}, "ERR_INVALID_ARG"),
+        ({"wfmt": 4, "n_out2": 8, "out2": (1 << 20) + 1, "ldo2": 8}, "ERR_ALIGNMENT"),
         ({"cfg_path": 4, "M": 8}, "ERR_INVALID_ARG"),                       # split-K needs the workspace
         ({"cfg_path": 4, "M": 8, "workspace": 1 << 20, "workspace_bytes": 100}, "ERR_INVALID_ARG"),
         ({"cfg_path": 4, "M": 8, "cfg_tiles": 3}, "ERR_INVALID_ARG"),

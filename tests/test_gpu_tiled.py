@@ -326,3 +326,39 @@ def test_gemv_tiled_graph_replays_bit_identical():
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 9])
+def test_gemv_tiled_second_store(m):
+    """out2 receives columns [0, n2) of the same launch's result bit for bit
+    (the query part of a QKV projection handed to the next kernel), at M
+    spanning two launches (9 = 8 + 1 rows), and leaves the rest of out2's
+    rows untouched."""
+    n, k, n2 = 6144, 2560, 4096
+    c = _int4_case(n, k, 900 + m)
+    tbuf, fmt = _tiled_i4(c, False)
+    x, g = _x(m, k, 901 + m), _gamma(k, 902 + m)
+    out = G.gemv(bf16_tensor(x), tbuf, fmt, n, gamma=bf16_tensor(g))
+    wide = torch.full((m, n2 + 24), -7.0, device="cuda", dtype=torch.bfloat16)
+    out2 = wide[:, 8: 8 + n2]
+    got = G.gemv(bf16_tensor(x), tbuf, fmt, n, gamma=bf16_tensor(g), out2=out2)
+    assert torch.equal(got, out)
+    assert torch.equal(out2, out[:, :n2])
+    assert bool((wide[:, :8] == -7).all()) and bool((wide[:, 8 + n2:] == -7).all())
+    ref = _ref(x, c.w_zp, g, O.EPI_NONE, None)
+    assert O.rel_err(f32(got), ref) <= TIGHT
+
+
+def test_gemv_tiled_second_store_paired_f32():
+    """The second store on a paired SiLU-gate GEMV with fp32 output and a
+    column count that is not a multiple of a row block (100 of 256)."""
+    n, k, m, n2 = 512, 1024, 2, 100
+    c = _fp8_case(n, k, 910)
+    tbuf, fmt = _tiled_f8(c, True)
+    x = _x(m, k, 911)
+    out = G.gemv(bf16_tensor(x), tbuf, fmt, n, epilogue=G.EPI_SILU_GATE, out_dtype=torch.float32)
+    out2 = torch.zeros(m, n2, device="cuda", dtype=torch.float32)
+    got = G.gemv(bf16_tensor(x), tbuf, fmt, n, epilogue=G.EPI_SILU_GATE, out_dtype=torch.float32, out2=out2)
+    assert torch.equal(got, out) and torch.equal(out2, out[:, :n2])
+    with pytest.raises(ValueError, match="out2"):
+        G.gemv(bf16_tensor(x), tbuf, fmt, n, epilogue=G.EPI_SILU_GATE, out2=torch.zeros(m, n2, device="cuda"))
