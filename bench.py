@@ -510,7 +510,8 @@ def pmc_summary(fetch_dir: str, write_dir: str) -> int:
             per.setdefault(key, [row["Kernel_Name"], 0.0])[1] += float(row["Counter_Value"])
         seq = [per[k] for k in sorted(per)]
         gemv = [(name, v) for name, v in seq if "gemv_" in name]
-        copy = [v for name, v in seq if "elementwise" in name.lower() and "mul" in name.lower()]
+        # the copies are the last three elementwise multiplies (earlier ones scale the synthetic weights)
+        copy = [v for name, v in seq if "elementwise" in name.lower() and "mul" in name.lower()][-3:]
         if len(gemv) != n * len(PROFILE_CASES) or not copy:
             raise SystemExit(f"{d}: {len(gemv)} GEMV dispatches (expected {n * len(PROFILE_CASES)}), "
                              f"{len(copy)} copy dispatches")
