@@ -326,24 +326,23 @@ def _table_keys():
     return sorted(json.loads(path.read_text()))
 
 
-@pytest.mark.parametrize("key", _table_keys())
-def test_table_launch_shapes_match_oracle(key):
-    """Every entry of the committed launch-shape table, run through gemv()'s
-    automatic selection, against the oracle."""
-    from breeze_amd import tuning
+def _bucket_floor(m_bucket: int) -> int:
+    """Smallest M that tuning.m_bucket maps to bucket ``m_bucket``."""
+    prev = {1: 0, 2: 1, 4: 2, 8: 4, 16: 8, 32: 16}[m_bucket]
+    return prev + 1
 
-    cfg = tuning.lookup(torch.device("cuda"), *[int(v) for v in key.split("|")[1:4]], int(key.split("|")[4]),
-                        key.split("|")[5] == "1", int(key.split("|")[6]))
-    assert cfg is not None, key
-    _, N, K, wfmt, epi, norm, M = (int(v) if i else v for i, v in enumerate(key.split("|")))
-    w, gamma, x = O.synth(N, K, M, seed=N + K)
+
+def _run_table_entry(key: str, M: int, group: int = 128):
+    _, N, K, wfmt, epi, norm, _ = (int(v) if i else v for i, v in enumerate(key.split("|")))
+    w, gamma, x = O.synth(N, K, M, seed=N + K + M)
     n_out = N // 2 if epi == 1 else N
     res_bits = O.f32_to_bf16_bits(np.random.default_rng(2).standard_normal((M, n_out)).astype(np.float32))
     res = bf16_tensor(res_bits) if epi == 2 else None
     g = bf16_tensor(gamma) if norm else None
     if wfmt == G.W_INT4_ZP:
-        c = Int4Case(w, 128, symmetric=True)
-        out = G.gemv(bf16_tensor(x), c.d_packed, wfmt, N, sc0=c.d_sz, group=128, gamma=g, epilogue=epi, residual=res)
+        c = Int4Case(w, group, symmetric=True)
+        out = G.gemv(bf16_tensor(x), c.d_packed, wfmt, N, sc0=c.d_sz, group=group, gamma=g, epilogue=epi,
+                     residual=res)
         w_eff = c.w_zp
     elif wfmt == G.W_FP8:
         c = Fp8Case(w)
@@ -356,4 +355,107 @@ def test_table_launch_shapes_match_oracle(key):
     xf = O.bf16_bits_to_f32(x)
     xn = O.rmsnorm_f32(xf, O.bf16_bits_to_f32(gamma)) if norm else xf
     ref = O.gemv_ref(xn, w_eff, epi, O.bf16_bits_to_f32(res_bits) if epi == 2 else None)
-    assert O.rel_err(f32(out), ref) <= TOL, key
+    return O.rel_err(f32(out), ref)
+
+
+@pytest.mark.parametrize("key", _table_keys())
+def test_table_launch_shapes_match_oracle(key):
+    """Every entry of the committed launch-shape table, run through gemv()'s
+    automatic selection at its bucket's own M, against the oracle."""
+    from breeze_amd import tuning
+
+    cfg = tuning.lookup(torch.device("cuda"), *[int(v) for v in key.split("|")[1:4]], int(key.split("|")[4]),
+                        key.split("|")[5] == "1", int(key.split("|")[6]))
+    assert cfg is not None, key
+    assert _run_table_entry(key, int(key.split("|")[6])) <= TOL, key
+
+
+@pytest.mark.parametrize("key", [k for k in _table_keys() if _bucket_floor(int(k.split("|")[6])) != int(k.split("|")[6])])
+def test_table_entries_at_smallest_m_of_bucket(key):
+    """tuning.m_bucket rounds M up, so an entry also drives every M down to
+    its bucket's floor (the M = 4 entries run M = 3, the M = 16 entries
+    M = 9): each entry at that smallest M, against the oracle."""
+    m = _bucket_floor(int(key.split("|")[6]))
+    assert _run_table_entry(key, m) <= TOL, (key, m)
+
+
+@pytest.mark.parametrize("key", [k for k in _table_keys() if k.split("|")[3] == "0"])
+def test_table_int4_entries_with_group_64(key):
+    """An int4 entry tuned for group 128 may force a matrix-core path that
+    group 64 cannot run: the wrapper must fall back to the built-in rule
+    instead of failing (at the bucket's M and at its floor)."""
+    mb = int(key.split("|")[6])
+    for m in sorted({mb, _bucket_floor(mb)}):
+        assert _run_table_entry(key, m, group=64) <= TOL, (key, m)
+
+
+# C4 points at full size the table and the tile tests leave out, in both
+# weight layouts: the tiled decode layout (streaming kernel, slices of <= 8
+# rows) and the row-major one (several-row split-K tile kernel)
+C4_FULL = [
+    ("fp8 K2560 N20480", "fp8", 20480, 2560, 4),
+    ("int4 K10240 N2560", "int4", 2560, 10240, 16),
+    ("fp8 K10240 N2560", "fp8", 2560, 10240, 16),
+]
+
+
+@pytest.mark.parametrize("layout", ["tiled", "rowmajor"])
+@pytest.mark.parametrize("name,fmt,n,k,m", C4_FULL, ids=[c[0] for c in C4_FULL])
+def test_c4_full_size(name, fmt, n, k, m, layout):
+    seed = sum(name.encode()) % 997
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x_bits = O.f32_to_bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    if fmt == "int4":
+        c = Int4Case(w, 128, symmetric=True)
+        w_eff = c.w_zp
+        if layout == "tiled":
+            wbuf = G.pack_tiled(G.W_INT4_ZP, c.d_packed, k, G.W_INT4_TILED, sc0=c.d_sz)
+            out = G.gemv(bf16_tensor(x_bits), wbuf, G.W_INT4_TILED, n)
+        else:
+            out = G.gemv(bf16_tensor(x_bits), c.d_packed, G.W_INT4_ZP, n, sc0=c.d_sz, group=128)
+    else:
+        c = Fp8Case(w)
+        w_eff = c.w_eff
+        if layout == "tiled":
+            wbuf = G.pack_tiled(G.W_FP8, c.d_codes, k, G.W_FP8_TILED, sc0=c.d_scale)
+            out = G.gemv(bf16_tensor(x_bits), wbuf, G.W_FP8_TILED, n)
+        else:
+            out = G.gemv(bf16_tensor(x_bits), c.d_codes, G.W_FP8, n, sc0=c.d_scale)
+    ref = O.gemv_ref(O.bf16_bits_to_f32(x_bits), w_eff)
+    assert O.rel_err(f32(out), ref) <= TOL
+
+
+# The C2/C3 and C5 projections at full size on the row-major kernels (the
+# tiled ones are covered by the tiled tests), M = 1 and 2
+ROWMAJOR_FULL = [
+    ("C2 down", "int4", 2560, 10240, False, 2),
+    ("C3 qkv", "fp8", 4096, 2560, True, 0),
+    ("C3 o_proj", "fp8", 2560, 4096, False, 2),
+    ("C3 down", "fp8", 2560, 10240, False, 2),
+    ("C5 qkv", "int4", 6144, 2560, True, 0),
+    ("C5 o_proj", "int4", 2560, 4096, False, 2),
+]
+
+
+@pytest.mark.parametrize("m", [1, 2])
+@pytest.mark.parametrize("name,fmt,n,k,norm,epi", ROWMAJOR_FULL, ids=[c[0] for c in ROWMAJOR_FULL])
+def test_rowmajor_full_size(name, fmt, n, k, norm, epi, m):
+    seed = sum(name.encode()) % 991
+    w, gamma, x = O.synth(n, k, m, seed=seed)
+    res_bits = O.f32_to_bf16_bits(np.random.default_rng(seed).standard_normal((m, n)).astype(np.float32))
+    g = bf16_tensor(gamma) if norm else None
+    res = bf16_tensor(res_bits) if epi == 2 else None
+    if fmt == "int4":
+        c = Int4Case(w, 128, symmetric=True)
+        out = G.gemv(bf16_tensor(x), c.d_packed, G.W_INT4_ZP, n, sc0=c.d_sz, group=128, gamma=g, epilogue=epi,
+                     residual=res)
+        w_eff = c.w_zp
+    else:
+        c = Fp8Case(w)
+        out = G.gemv(bf16_tensor(x), c.d_codes, G.W_FP8, n, sc0=c.d_scale, gamma=g, epilogue=epi, residual=res)
+        w_eff = c.w_eff
+    xf = O.bf16_bits_to_f32(x)
+    xn = O.rmsnorm_f32(xf, O.bf16_bits_to_f32(gamma)) if norm else xf
+    ref = O.gemv_ref(xn, w_eff, epi, O.bf16_bits_to_f32(res_bits) if epi == 2 else None)
+    assert O.rel_err(f32(out), ref) <= TOL
