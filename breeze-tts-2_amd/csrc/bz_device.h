@@ -145,6 +145,14 @@ constexpr uint32_t kBufferOob = 0xFFFFFFF0u;  // an offset past any buffer_rsrc 
 __device__ __forceinline__ u32x4 buffer_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
+// The same with the non-temporal hint (cache-policy operand 2 = nt on gfx950),
+// for data read once.
+__device__ __forceinline__ u32x4 buffer_ld16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);
+}
+__device__ __forceinline__ uint32_t buffer_ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 

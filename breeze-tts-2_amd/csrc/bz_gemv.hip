@@ -66,7 +66,13 @@ static int check_desc(const bz_gemv_desc* d, DescInfo& di) {
             if (d->residual_dtype != BZ_DT_BF16 && d->residual_dtype != BZ_DT_F32) return BZ_ERR_INVALID_ARG;
         }
         if (tiled_paired(wf) != (epi == BZ_EPI_SILU_GATE)) return BZ_ERR_UNSUPPORTED;
-        if (d->cfg_path && d->cfg_path != PATH_STREAM) return BZ_ERR_UNSUPPORTED;
+        // the streaming kernel (path 5), or the several-row tile kernel (path 4)
+        // for unpaired weights without the second store
+        if (d->cfg_path == PATH_TILE) {
+            if (tiled_paired(wf) || d->n_out2) return BZ_ERR_UNSUPPORTED;
+        } else if (d->cfg_path && d->cfg_path != PATH_STREAM) {
+            return BZ_ERR_UNSUPPORTED;
+        }
         if (N % 16 || !tiled_units(wf, K) || (tiled_i4(wf) && d->group != 128)) return BZ_ERR_SHAPE;
         const int n_out = epi == BZ_EPI_SILU_GATE ? N / 2 : N;
         if (d->ldx < K || d->ldo < n_out) return BZ_ERR_INVALID_ARG;
@@ -146,7 +152,7 @@ static int tile_plan(const bz_gemv_desc* d, const DescInfo& di, int M, TilePlan&
     const int K = d->K, wf = d->wfmt;
     const bool forced = d->cfg_path == PATH_TILE;
     if (d->gamma || d->epilogue == BZ_EPI_SILU_GATE) return BZ_ERR_UNSUPPORTED;
-    const int UK = mfma_unit_k(wf);
+    const int UK = tile_unit_k(wf);
     if ((di.i4 && d->group < 128) || K % UK || di.row_bytes >= (1 << 24)) return BZ_ERR_UNSUPPORTED;
     // 32-bit offsets inside the kernel: x rows of a launch, a slice of partials
     if ((int64_t)M * d->ldx >= (int64_t(1) << 31) || (int64_t)M * di.n_out >= (int64_t(1) << 31))
@@ -184,7 +190,10 @@ static int tile_plan(const bz_gemv_desc* d, const DescInfo& di, int M, TilePlan&
 // The automatic rule takes the tile kernel from this many rows on.
 constexpr int kTileMinRows = 5;
 
-static bool tile_auto(const bz_gemv_desc* d) { return d->cfg_path == 0 && d->M >= kTileMinRows; }
+// (Tiled formats: unpaired weights only, and not with the second store.)
+static bool tile_auto(const bz_gemv_desc* d) {
+    return d->cfg_path == 0 && d->M >= kTileMinRows && !d->n_out2 && !tiled_paired(d->wfmt);
+}
 
 static int launch_tile(int wf, const TileParams& tp, const TileLaunch& l, hipStream_t st) {
     switch (wf) {
@@ -192,6 +201,8 @@ static int launch_tile(int wf, const TileParams& tp, const TileLaunch& l, hipStr
         case WF_I4MIN: return launch_tile_i4min(tp, l, st);
         case WF_FP8: return launch_tile_fp8(tp, l, st);
         case WF_BF16: return launch_tile_bf16(tp, l, st);
+        case BZ_W_INT4_TILED: return launch_tile_i4t(tp, l, st);
+        case BZ_W_FP8_TILED: return launch_tile_f8t(tp, l, st);
         default: return BZ_ERR_INVALID_ARG;
     }
 }
@@ -216,7 +227,9 @@ static int stream_plan(const bz_gemv_desc* d, int rows, StreamLaunch& l) {
             break;
         }
     if (!upw) return BZ_ERR_UNSUPPORTED;  // K too long for the waves
-    if (!d->cfg_waves) nw = (NU + upw - 1) / upw;
+    // every wave owns at least one unit (a forced wave count above that is
+    // lowered): a wave reads the staged x of its own units only
+    nw = std::min(nw, (NU + upw - 1) / upw);
     l.nw = nw;
     l.upw = upw;
     l.mm = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
@@ -285,7 +298,6 @@ using namespace bz;
 extern "C" size_t bz_gemv_workspace(const bz_gemv_desc* d) {
     DescInfo di;
     if (check_desc(d, di) != BZ_OK) return 0;
-    if (is_tiled(d->wfmt)) return 0;
     if (d->cfg_path != PATH_TILE && !tile_auto(d)) return 0;
     TilePlan pl{};
     return tile_plan(d, di, std::min(d->M, kTileMaxRows), pl) == BZ_OK ? pl.ws : 0;
@@ -296,7 +308,7 @@ extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
     const int rc0 = check_desc(d, di);
     if (rc0 != BZ_OK) return rc0;
     const int M = d->M, N = d->N, K = d->K, wf = d->wfmt, epi = d->epilogue;
-    if (is_tiled(wf)) return gemv_tiled(d, di, static_cast<hipStream_t>(stream));
+    const bool tiled = is_tiled(wf);
     const int n_out = di.n_out, glog2 = di.glog2;
     const int64_t row_bytes = di.row_bytes;
     const bool i4 = di.i4;
@@ -339,6 +351,8 @@ extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
             p.res_f32 = d->residual_dtype == BZ_DT_F32;
             p.norm = 0;
             tp.cnt = static_cast<uint32_t*>(d->workspace);
+            tp.NU = tiled ? tiled_units(wf, K) : 0;
+            tp.chunk = tiled ? (int64_t)tiled_chunk_bytes(wf, tp.NU) : 0;
             // the plan of a last, shorter launch (checked before anything is launched)
             TilePlan pl_rem = pl;
             if (M > kTileMaxRows && M % kTileMaxRows && tile_plan(d, di, M % kTileMaxRows, pl_rem) != BZ_OK)
@@ -369,6 +383,7 @@ extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
             return BZ_OK;
         }
     }
+    if (tiled) return gemv_tiled(d, di, static_cast<hipStream_t>(stream));
 
     const bool silu = epi == BZ_EPI_SILU_GATE;
     const int T = silu ? 2 : 1;

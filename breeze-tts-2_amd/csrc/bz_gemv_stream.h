@@ -201,21 +201,20 @@ __global__ void __launch_bounds__(1024) gemv_stream(StreamParams p) {
         rs0 = rsc[c];
         if (PAIR) rs1 = rsc[c + 8];
     }
-    // int4: the (s, z) pairs of this lane's row for the wave's units
+    // The wave's UPW tiles and, for int4, the (s, z) pairs of this lane's row,
+    // through range-checked buffer loads over the block's tiles and scales:
+    // a unit past the block (the last wave may own fewer than UPW) reads as
+    // zeros without a memory request and adds exactly 0 (zero codes, s = z =
+    // 0), so every wave runs the same branch-free loop with exact wait counts
+    const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(chunk, (uint32_t)NU * 1024u);
     uint32_t sc[UPW];
     if (I4) {
+        const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(chunk + (int64_t)NU * 1024, (uint32_t)NU * 64u);
 #pragma unroll
-        for (int q = 0; q < UPW; ++q) {
-            const int u = min(u0 + q, NU - 1);
-            sc[q] = *reinterpret_cast<const uint32_t*>(chunk + (int64_t)NU * 1024 + u * 64 + j * 4);
-        }
+        for (int q = 0; q < UPW; ++q) sc[q] = buffer_ld4(srs, (uint32_t)(u0 + q) * 64u + j * 4);
     }
     u32x4 wv[UPW];
-    auto issue = [&](int q) {
-        const int u = min(u0 + q, NU - 1);
-        wv[q] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(chunk + (int64_t)u * 1024 + j * 64 + kq * 16));
-    };
+    auto issue = [&](int q) { wv[q] = buffer_ld16_nt(wrs, (uint32_t)(u0 + q) * 1024u + j * 64 + kq * 16); };
 #pragma unroll
     for (int q = 0; q < D; ++q) issue(q);
     __builtin_amdgcn_sched_barrier(0);
@@ -300,15 +299,17 @@ __global__ void __launch_bounds__(1024) gemv_stream(StreamParams p) {
     // complete in order, so no workgroup barrier is needed here
     __builtin_amdgcn_wave_barrier();
 
-    // 2. the wave's units: consume tile q, issue tile q + D.  Every wave but
-    //    possibly the last has all UPW units; that case runs without run-time
-    //    conditions, so each wait counts exactly the loads in flight.
+    // 2. the wave's units: consume tile q, issue tile q + D, without run-time
+    //    conditions, so each wait counts exactly the loads in flight.  A unit
+    //    past the block reads x and X at the block's last unit, which the
+    //    same wave staged (every wave owns at least one unit), so it
+    //    multiplies finite values by its zero weights.
     float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     f32x4_t facc = {0.0f, 0.0f, 0.0f, 0.0f};
     const uint8_t* xa = xs + min(j, M - 1) * xrow;  // the x row this lane supplies to A
     const NibbleConsts nc;
     auto consume = [&](int q, bool next) {
-        const int u = u0 + q;
+        const int u = min(u0 + q, NU - 1);
         if (I4) {
             u32x4 bq[4];
 #pragma unroll
@@ -345,14 +346,8 @@ __global__ void __launch_bounds__(1024) gemv_stream(StreamParams p) {
             facc = mfma_bf16(*reinterpret_cast<const u32x4*>(xu + 16), b1, facc);
         }
     };
-    if (nu == UPW) {
 #pragma unroll
-        for (int q = 0; q < UPW; ++q) consume(q, q + D < UPW);
-    } else {
-#pragma unroll
-        for (int q = 0; q < UPW; ++q)
-            if (q < nu) consume(q, q + D < nu);
-    }
+    for (int q = 0; q < UPW; ++q) consume(q, q + D < UPW);
     if (!I4) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) y[r] = facc[r];

@@ -51,7 +51,20 @@ struct TileParams {
     int nsl;    // K slices
     uint32_t* cnt;
     float* part;
+    int64_t chunk;  // tiled formats: bytes per 16-row block
+    int NU;         // tiled formats: units per row (K / unit k)
 };
+
+// Formats the tile kernel reads: the row-major ones (WF_I4ZP, WF_I4MIN,
+// WF_FP8, WF_BF16) and the unpaired tiled formats (include/bz_gemv.h), whose
+// 1 KiB tiles are exactly this kernel's per-wave unit loads (16 rows x 64
+// bytes) made contiguous, with the int4 (s, z) pairs and fp8 row scales at
+// the end of each 16-row block.
+__host__ __device__ constexpr bool tile_tiled(int wf) { return wf == BZ_W_INT4_TILED || wf == BZ_W_FP8_TILED; }
+__host__ __device__ constexpr bool tile_i4(int wf) { return is_int4(wf) || wf == BZ_W_INT4_TILED; }
+__host__ __device__ constexpr bool tile_f8(int wf) { return wf == WF_FP8 || wf == BZ_W_FP8_TILED; }
+__host__ __device__ constexpr bool tile_zp(int wf) { return wf == WF_I4ZP || wf == BZ_W_INT4_TILED; }
+__host__ __device__ constexpr int tile_unit_k(int wf) { return tile_i4(wf) ? 128 : (tile_f8(wf) ? 64 : 32); }
 
 struct TileLaunch {
     int MB, T, D, nw;
@@ -72,7 +85,7 @@ __host__ __device__ inline TileLds tile_lds_layout(int M, int MB, int ks, int wf
     TileLds L;
     L.xs = 0;
     L.x128 = align16(M * tile_xrow(ks) * 2);
-    L.flag = L.x128 + (is_int4(wf) ? align16((ks / 128) * 16 * MB * 4) : 0);
+    L.flag = L.x128 + (tile_i4(wf) ? align16((ks / 128) * 16 * MB * 4) : 0);
     L.total = L.flag + 16;
     return L;
 }
@@ -84,7 +97,7 @@ __host__ __device__ inline TileLds tile_lds_layout(int M, int MB, int ks, int wf
 template <int WF>
 __device__ __forceinline__ void tile_stage(u32x4 v, int m, int kq, uint16_t* xs, float* x128, int xrow, int rstride) {
     u32x4 o = v;
-    if (is_int4(WF)) {
+    if (tile_i4(WF)) {
         o[0] = (v[0] & 0xFFFFu) | (v[2] << 16);
         o[1] = (v[0] >> 16) | (v[2] & 0xFFFF0000u);
         o[2] = (v[1] & 0xFFFFu) | (v[3] << 16);
@@ -99,8 +112,11 @@ __device__ __forceinline__ void tile_stage(u32x4 v, int m, int kq, uint16_t* xs,
 
 // Epilogue of one output: fp8 row scale, residual, store.
 template <int WF>
-__device__ __forceinline__ void tile_store(const GemvParams& p, float v, int r, int c) {
+__device__ __forceinline__ void tile_store(const TileParams& tp, float v, int r, int c) {
+    const GemvParams& p = tp.p;
     if (WF == WF_FP8) v *= reinterpret_cast<const float*>(p.sc0)[c];
+    if (WF == BZ_W_FP8_TILED)
+        v *= reinterpret_cast<const float*>(p.w + (int64_t)(c >> 4) * tp.chunk + (int64_t)tp.NU * 1024)[c & 15];
     if (p.epi == BZ_EPI_RESIDUAL) {
         const int64_t idx = (int64_t)r * p.ldr + c;
         v += p.res_f32 ? reinterpret_cast<const float*>(p.res)[idx]
@@ -154,7 +170,7 @@ __device__ __forceinline__ void tile_sum_slices(const TileParams& tp, int cb, in
             if (i >= nout) continue;
             const int r = i >> cbw_log2;
             const int c = cb * CBW + (i - r * CBW);
-            if (c < p.n_out) tile_store<WF>(p, sum[q], r, c);
+            if (c < p.n_out) tile_store<WF>(tp, sum[q], r, c);
         }
     }
 }
@@ -163,7 +179,7 @@ template <int WF, int MB, int T, int D>
 __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const GemvParams& p = tp.p;
-    constexpr int UK = mfma_unit_k(WF);
+    constexpr int UK = tile_unit_k(WF);
     constexpr int RS = 16 * MB;  // x128 row stride (rows per unit)
     const int nthr = blockDim.x, NW = nthr >> 6;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -220,7 +236,8 @@ __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         const int lr = min(j, max(p.n_out - 1 - (col0 + 16 * t), 0));
-        loff[t] = __umul24((uint32_t)lr, (uint32_t)p.row_bytes) + (uint32_t)(kb * 16);
+        loff[t] = tile_tiled(WF) ? (uint32_t)(j * 64 + kb * 16)
+                                 : __umul24((uint32_t)lr, (uint32_t)p.row_bytes) + (uint32_t)(kb * 16);
         const int row = min(col0 + 16 * t + j, p.n_out - 1);
         soff[t] = WF == WF_I4ZP ? (uint32_t)row : (uint32_t)row * (uint32_t)p.G;
     }
@@ -230,6 +247,14 @@ __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int ct = min(col0 + 16 * t, p.n_out - 1);
+            if (tile_tiled(WF)) {
+                // the tile of unit u in the 16-row block of column ct (uniform), its scales after the tiles
+                const uint8_t* blk = p.w + (int64_t)(ct >> 4) * tp.chunk;
+                buf[d][t] = ldg16(blk + (int64_t)u * 1024 + loff[t]);
+                if (tile_i4(WF))
+                    scb[d][t] = *reinterpret_cast<const uint32_t*>(blk + (int64_t)tp.NU * 1024 + u * 64 + j * 4);
+                continue;
+            }
             const uint8_t* base = p.w + (int64_t)ct * p.row_bytes + (int64_t)u * 64;  // uniform
             buf[d][t] = ldg16(base + loff[t]);
             if (WF == WF_I4ZP) {
@@ -267,11 +292,11 @@ __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
     const uint16_t* xa[MB];  // this lane's A row (clamped to the last row of x) at its 16-byte slot
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
-        xa[mb] = xs + min(16 * mb + j, M - 1) * xrow + kb * (is_int4(WF) ? 32 : (WF == WF_FP8 ? 16 : 8));
+        xa[mb] = xs + min(16 * mb + j, M - 1) * xrow + kb * (tile_i4(WF) ? 32 : (tile_f8(WF) ? 16 : 8));
     const NibbleConsts nc;
     auto consume = [&](int d, StepCursor c) {
         const int u = c.ch;
-        if (is_int4(WF)) {
+        if (tile_i4(WF)) {
             u32x4 a[MB][4];
             f32x4_t X[MB];
 #pragma unroll
@@ -295,13 +320,13 @@ __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
                 }
                 const uint32_t e = scb[d][t];
                 const float s = bf16_lo(e);
-                const float zp = bf16_hi(e) - (WF == WF_I4ZP ? 136.0f : 128.0f) * s;
+                const float zp = bf16_hi(e) - (tile_zp(WF) ? 136.0f : 128.0f) * s;
 #pragma unroll
                 for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
                     for (int q = 0; q < 4; ++q) acc[t][mb][q] += s * dacc[mb][q] + zp * X[mb][q];
             }
-        } else if (WF == WF_FP8) {
+        } else if (tile_f8(WF)) {
             u32x4 a0[MB], a1[MB];
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
@@ -346,7 +371,7 @@ __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int r = 16 * mb + 4 * kb + q;
-                    if (r < M) tile_store<WF>(p, acc[t][mb][q], r, c);
+                    if (r < M) tile_store<WF>(tp, acc[t][mb][q], r, c);
                 }
         }
         return;
@@ -431,5 +456,7 @@ int launch_tile_i4zp(const TileParams& tp, const TileLaunch& l, hipStream_t st);
 int launch_tile_i4min(const TileParams& tp, const TileLaunch& l, hipStream_t st);
 int launch_tile_fp8(const TileParams& tp, const TileLaunch& l, hipStream_t st);
 int launch_tile_bf16(const TileParams& tp, const TileLaunch& l, hipStream_t st);
+int launch_tile_i4t(const TileParams& tp, const TileLaunch& l, hipStream_t st);
+int launch_tile_f8t(const TileParams& tp, const TileLaunch& l, hipStream_t st);
 
 }  // namespace bz

@@ -117,7 +117,9 @@ def _desc(L, **kw):
         ({"wfmt": 4, "K": 192, "ldx": 192}, "ERR_SHAPE"),      # int4 unit = 128 k
         ({"wfmt": 4, "group": 64}, "ERR_SHAPE"),               # tiled int4 is group 128
         ({"wfmt": 6, "K": 160, "ldx": 160}, "ERR_SHAPE"),      # fp8 unit = 64 k
-        ({"wfmt": 4, "cfg_path": 2}, "ERR_UNSUPPORTED"),       # tiled formats run path 5 only
+        ({"wfmt": 4, "cfg_path": 2}, "ERR_UNSUPPORTED"),       # tiled formats run paths 4 and 5 only
+        ({"wfmt": 5, "epilogue": 1, "cfg_path": 4}, "ERR_UNSUPPORTED"),  # paired: streaming path only
+        ({"wfmt": 4, "cfg_path": 4, "n_out2": 8, "out2": 1 << 20, "ldo2": 8}, "ERR_UNSUPPORTED"),  # no second store
         ({"cfg_path": 5}, "ERR_UNSUPPORTED"),                  # path 5 reads tiled formats only
         ({"cfg_path": 6}, "ERR_INVALID_ARG"),
         ({"reserved0": 1}, "ERR_INVALID_ARG"),

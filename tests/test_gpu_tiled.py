@@ -362,3 +362,69 @@ def test_gemv_tiled_second_store_paired_f32():
     assert torch.equal(got, out) and torch.equal(out2, out[:, :n2])
     with pytest.raises(ValueError, match="out2"):
         G.gemv(bf16_tensor(x), tbuf, fmt, n, epilogue=G.EPI_SILU_GATE, out2=torch.zeros(m, n2, device="cuda"))
+
+
+# ---------------------------------------------------------------------------
+# several rows: the tile kernel over the tiled formats
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("fmt", ["int4", "fp8"])
+@pytest.mark.parametrize("m", [5, 8, 9, 16, 17, 32, 40])
+def test_tile_kernel_reads_tiled_formats(fmt, m):
+    """From M = 5 on (no RMSNorm, no SiLU-gate) a tiled weight takes the
+    several-row tile kernel, which reads its tiles in place: the result is
+    bit-identical to the same kernel over the row-major weight (same launch
+    plan, same arithmetic) and within the bar of the oracle."""
+    n, k = 2560, 2560
+    c = _int4_case(n, k, 950 + m) if fmt == "int4" else _fp8_case(n, k, 960 + m)
+    tbuf, tf = _tiled_i4(c, False) if fmt == "int4" else _tiled_f8(c, False)
+    x = _x(m, k, 970 + m)
+    res = _x(m, n, 980 + m)
+    got = G.gemv(bf16_tensor(x), tbuf, tf, n, epilogue=G.EPI_RESIDUAL, residual=bf16_tensor(res), cfg=(0, 0, 0, 4))
+    if fmt == "int4":
+        want = G.gemv(bf16_tensor(x), c.d_packed, G.W_INT4_ZP, n, sc0=c.d_sz, epilogue=G.EPI_RESIDUAL,
+                      residual=bf16_tensor(res), cfg=(0, 0, 0, 4))
+        w_eff = c.w_zp
+    else:
+        want = G.gemv(bf16_tensor(x), c.d_codes, G.W_FP8, n, sc0=c.d_scale, epilogue=G.EPI_RESIDUAL,
+                      residual=bf16_tensor(res), cfg=(0, 0, 0, 4))
+        w_eff = c.w_eff
+    assert torch.equal(got, want)
+    auto = G.gemv(bf16_tensor(x), tbuf, tf, n, epilogue=G.EPI_RESIDUAL, residual=bf16_tensor(res))
+    assert torch.equal(auto, got)   # the automatic choice from M = 5 on
+    assert O.rel_err(f32(got), _ref(x, w_eff, None, O.EPI_RES, res)) <= TIGHT
+
+
+@pytest.mark.parametrize("slices", [4, 5, 8])
+def test_tile_kernel_tiled_forced_slices(slices):
+    """Forced K slices (split-K partials and the last arrival's sum) over a
+    tiled int4 weight, K10240 N2560 (down) at M = 16, against the row-major
+    weight through the same plan."""
+    n, k, m = 2560, 10240, 16
+    c = _int4_case(n, k, 990)
+    tbuf, tf = _tiled_i4(c, False)
+    x = bf16_tensor(_x(m, k, 991))
+    cfg = (0, 0, 0, 4, slices)
+    got = G.gemv(x, tbuf, tf, n, cfg=cfg)
+    want = G.gemv(x, c.d_packed, G.W_INT4_ZP, n, sc0=c.d_sz, cfg=cfg)
+    assert torch.equal(got, want)
+    assert O.rel_err(f32(got), _ref(_x(m, k, 991), c.w_zp, None, O.EPI_NONE, None)) <= TIGHT
+
+
+def test_tile_kernel_not_taken_with_norm_silu_or_second_store():
+    """RMSNorm, SiLU-gate and the second store stay on the streaming kernel
+    at any M (the tile kernel has none of them); forcing path 4 for a paired
+    weight is refused."""
+    n, k, m = 512, 1024, 12
+    c = _int4_case(n, k, 995)
+    tp, tfp = _tiled_i4(c, True)
+    x, g = _x(m, k, 996), _gamma(k, 997)
+    out = G.gemv(bf16_tensor(x), tp, tfp, n, gamma=bf16_tensor(g), epilogue=G.EPI_SILU_GATE)
+    assert O.rel_err(f32(out), _ref(x, c.w_zp, g, O.EPI_SILU, None)) <= TIGHT
+    with pytest.raises(RuntimeError, match="status 4"):
+        G.gemv(bf16_tensor(x), tp, tfp, n, gamma=bf16_tensor(g), epilogue=G.EPI_SILU_GATE, cfg=(0, 0, 0, 4))
+    t, tf = _tiled_i4(c, False)
+    out2 = torch.zeros(m, 64, device="cuda", dtype=torch.bfloat16)
+    out = G.gemv(bf16_tensor(x), t, tf, n, out2=out2)
+    assert torch.equal(out2, out[:, :64])
