@@ -542,6 +542,17 @@ def pmc_summary(fetch_dir: str, write_dir: str) -> int:
 
 
 FLOOR_MIB = (13, 26, 52)
+# (label, bytes, bytes per workgroup): the tiled decode weights read with
+# their own kernel's decomposition (one workgroup per 16-row block) and with
+# more, smaller chunks per workgroup
+FLOOR_CHUNKS = [
+    ("int4 down K10240 N2560, 160 blocks", 13926400, 87040),
+    ("int4 down bytes, 320 workgroups", 13926400, 43520),
+    ("int4 down bytes, 850 workgroups", 13926400, 16384),
+    ("int4 gate|up K2560 N20480, 1280 blocks", 27852800, 21760),
+    ("fp8 down K10240 N2560, 160 blocks", 26234880, 163968),
+    ("fp8 down bytes, 640 workgroups", 26234880, 40992),
+]
 
 
 def floors(torch, G, dev, log) -> dict:
@@ -550,31 +561,45 @@ def floors(torch, G, dev, log) -> dict:
       empty_node_us  one empty workgroup (bz_stream_read with no bytes),
                      launched back to back in a graph;
       read           bz_stream_read (non-temporal 16-byte loads, nothing
-                     written) over 13, 26 and 52 MiB -- the sizes of the int4
-                     down, int4 gate|up and fp8 gate|up weights -- rotating
-                     through >= 1 GiB, with the line t = fixed + bytes / rate
-                     fitted through the three points;
+                     written, 16 KiB per workgroup) over 13, 26 and 52 MiB --
+                     the sizes of the int4 down, int4 gate|up and fp8 gate|up
+                     weights -- rotating through >= 1 GiB, with the line
+                     t = fixed + bytes / rate fitted through the three points;
+      chunks         the same read with the decode GEMVs' own decomposition
+                     (one workgroup per 16-row block of a tiled weight) and
+                     with more workgroups, at their byte counts;
       copy_1gib      torch's device-to-device copy of 1 GiB (read + write)."""
     from breeze_amd.fused.kernels import graph_time_us
 
     sink = torch.zeros(4, dtype=torch.int32, device=dev)
     empty = graph_time_us(lambda: G.stream_read(None, sink), iters=256)
-    reads = []
-    for mib in FLOOR_MIB:
-        size = mib << 20
+
+    def timed_read(size, chunk):
         ncopy = max(2, -(-(1 << 30) // size))
         pool = torch.randint(0, 1 << 30, (ncopy * size // 4,), dtype=torch.int32, device=dev)
         bufs = [pool[i * size // 4:(i + 1) * size // 4] for i in range(ncopy)]
         st = {"i": 0}
 
         def fn():
-            G.stream_read(bufs[st["i"] % ncopy], sink)
+            G.stream_read(bufs[st["i"] % ncopy], sink, chunk=chunk)
             st["i"] += 1
 
         us = graph_time_us(fn, iters=min(2 * ncopy, 256))
+        del pool, bufs
+        return us
+
+    reads = []
+    for mib in FLOOR_MIB:
+        size = mib << 20
+        us = timed_read(size, 16384)
         reads.append({"mib": mib, "bytes": size, "us": round(us, 3), "gbps": round(size / us / 1e3, 1)})
         log(f"read floor {mib} MiB: {us:.2f} us ({size / us / 1e3:.0f} GB/s)")
-        del pool, bufs
+    chunks = []
+    for label, size, chunk in FLOOR_CHUNKS:
+        us = timed_read(size, chunk)
+        chunks.append({"what": label, "bytes": size, "chunk": chunk, "workgroups": size // chunk, "us": round(us, 3),
+                       "gbps": round(size / us / 1e3, 1)})
+        log(f"read {label} ({size // chunk} x {chunk} B): {us:.2f} us ({size / us / 1e3:.0f} GB/s)")
     xs = [r["bytes"] for r in reads]
     ys = [r["us"] for r in reads]
     xm, ym = sum(xs) / len(xs), sum(ys) / len(ys)
@@ -597,7 +622,7 @@ def floors(torch, G, dev, log) -> dict:
     log(f"empty node {empty:.2f} us; read line {fixed:.2f} us + bytes at {1 / slope / 1e3:.0f} GB/s; "
         f"1 GiB copy {copy_us:.0f} us ({2 * (1 << 30) / copy_us / 1e3:.0f} GB/s read+write)")
     return {"empty_node_us": round(empty, 3), "read": reads,
-            "read_fit": {"fixed_us": round(fixed, 3), "gbps": round(1 / slope / 1e3, 1)},
+            "read_fit": {"fixed_us": round(fixed, 3), "gbps": round(1 / slope / 1e3, 1)}, "chunks": chunks,
             "copy_1gib": {"us": round(copy_us, 1), "gbps_read_plus_write": round(2 * (1 << 30) / copy_us / 1e3, 1)}}
 
 

@@ -139,7 +139,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.bz_attn_default_split.restype = ctypes.c_int32
     lib.bz_attn_default_split.argtypes = [i32]
     lib.bz_stream_read.restype = ctypes.c_int
-    lib.bz_stream_read.argtypes = [vp, ctypes.c_size_t, ctypes.c_uint32, vp, vp]
+    lib.bz_stream_read.argtypes = [vp, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_uint32, vp, vp]
     lib.bz_sample_cfg.restype = ctypes.c_int
     lib.bz_sample_cfg.argtypes = [vp, i64, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
 

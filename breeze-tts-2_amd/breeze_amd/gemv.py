@@ -359,15 +359,16 @@ def gemv_traceable(x, w, wfmt, n, *, sc0=None, sc1=None, group=128, gamma=None, 
                 epilogue=epilogue, residual=residual, out_dtype=out_dtype)
 
 
-def stream_read(buf: Optional[torch.Tensor], sink: torch.Tensor, key: int = 0x9E3779B9) -> None:
-    """Launch the read-floor kernel over ``buf`` (bytes a multiple of 16 KiB;
-    None: one empty workgroup).  ``sink`` is an int32 device tensor, written
-    only if a thread's XOR of its data equals ``key``."""
+def stream_read(buf: Optional[torch.Tensor], sink: torch.Tensor, chunk: int = 16384, key: int = 0x9E3779B9) -> None:
+    """Launch the read-floor kernel over ``buf`` (one workgroup per ``chunk``
+    contiguous bytes; the bytes a multiple of it; None: one empty
+    workgroup).  ``sink`` is an int32 device tensor, written only if a
+    thread's XOR of its data equals ``key``."""
     _require_gpu("sink", sink, sink.device)
     nbytes = 0 if buf is None else buf.numel() * buf.element_size()
     if buf is not None and not buf.is_contiguous():
         raise ValueError("buf must be contiguous")
-    _lib.check(_lib.lib().bz_stream_read(_ptr(buf), nbytes, key, sink.data_ptr(), _lib.stream_of(sink)),
+    _lib.check(_lib.lib().bz_stream_read(_ptr(buf), nbytes, chunk, key, sink.data_ptr(), _lib.stream_of(sink)),
                "bz_stream_read")
 
 

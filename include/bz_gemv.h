@@ -188,11 +188,14 @@ size_t bz_gemv_workspace(const bz_gemv_desc* d);
 int bz_gemv(const bz_gemv_desc* d, void* stream);
 
 /* Measurement aid, no counterpart in the reference: reads `bytes` (a
- * multiple of 16 KiB, 16-byte aligned) from device memory `p` once and
+ * multiple of `chunk`, which is a multiple of 16 and at most 256 KiB;
+ * 16-byte aligned) from device memory `p` once, one workgroup per
+ * contiguous `chunk` bytes (1 KiB tiles, about 4 per wave), and
  * writes nothing unless the XOR a thread read equals `key` (then `*sink`).
- * Its duration is the streaming-read floor the GEMVs are compared with;
- * bytes = 0 launches one empty workgroup (the fixed cost of a launch). */
-int bz_stream_read(const void* p, size_t bytes, uint32_t key, uint32_t* sink, void* stream);
+ * Its duration is the streaming-read floor the GEMVs are compared with, for
+ * the same bytes per workgroup; bytes = 0 launches one empty workgroup (the
+ * fixed cost of a launch). */
+int bz_stream_read(const void* p, size_t bytes, size_t chunk, uint32_t key, uint32_t* sink, void* stream);
 
 /* Size of bz_gemv_noalloc's static device workspace, per GPU. */
 #define BZ_GEMV_SCRATCH_BYTES ((size_t)8 << 20)

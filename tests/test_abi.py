@@ -440,3 +440,15 @@ def test_gemv_noalloc_refuses_before_touching_the_gpu(L):
     header = HEADER.read_text()
     assert re.search(r"#define BZ_GEMV_SCRATCH_BYTES \(\(size_t\)8 << 20\)", header)
     assert L.GEMV_SCRATCH_BYTES == 8 << 20
+
+
+def test_stream_read_validation(L):
+    """The read-floor kernel's argument checks (no launch happens)."""
+    lib = L.lib()
+    fake = 1 << 20
+    assert lib.bz_stream_read(fake, 4096, 1024, 0, None, None) == L.ERR_INVALID_ARG     # no sink
+    assert lib.bz_stream_read(None, 4096, 1024, 0, fake, None) == L.ERR_INVALID_ARG     # no buffer
+    assert lib.bz_stream_read(fake, 4096, 0, 0, fake, None) == L.ERR_INVALID_ARG        # no chunk
+    assert lib.bz_stream_read(fake, 4096, 1000, 0, fake, None) == L.ERR_SHAPE           # bytes % chunk
+    assert lib.bz_stream_read(fake, 4104, 1368, 0, fake, None) == L.ERR_SHAPE           # chunk % 16
+    assert lib.bz_stream_read(fake + 8, 4096, 1024, 0, fake, None) == L.ERR_ALIGNMENT

@@ -428,3 +428,19 @@ def test_tile_kernel_not_taken_with_norm_silu_or_second_store():
     out2 = torch.zeros(m, 64, device="cuda", dtype=torch.bfloat16)
     out = G.gemv(bf16_tensor(x), t, tf, n, out2=out2)
     assert torch.equal(out2, out[:, :64])
+
+
+def test_stream_read_writes_only_on_key_match():
+    """The read-floor kernel reads every chunk and writes its sink only when a
+    thread's XOR equals the key: zeros with key 1 leave the sink alone, key 0
+    writes 0; an empty launch writes nothing."""
+    buf = torch.zeros(850 * 16384 // 4, dtype=torch.int32, device="cuda")
+    sink = torch.full((4,), 7, dtype=torch.int32, device="cuda")
+    G.stream_read(buf, sink, chunk=16384, key=1)
+    G.stream_read(buf, sink, chunk=16384 * 5, key=1)
+    G.stream_read(None, sink)
+    torch.cuda.synchronize()
+    assert sink.tolist() == [7, 7, 7, 7]
+    G.stream_read(buf, sink, chunk=16384 * 10, key=0)
+    torch.cuda.synchronize()
+    assert sink.tolist() == [0, 7, 7, 7]
