@@ -175,8 +175,6 @@ __global__ void __launch_bounds__(kRopeThreads) qkv_rope_cache_kernel(
 // ---------------------------------------------------------------------------
 // Decode attention: one workgroup per (batch row b, kv head j, split sp).
 // ---------------------------------------------------------------------------
-constexpr int kAttnWaves = 4;
-constexpr int kAttnThreads = 64 * kAttnWaves;
 constexpr int kBlk = 16;           // positions per block (the MFMA's 16 columns)
 constexpr int kUnsplitMax = 192;   // attended positions up to which a call runs unsplit
 constexpr float kNegBig = -1e30f;  // initial running max, as the reference
@@ -351,11 +349,13 @@ __device__ __forceinline__ float bcast(float v, int lane) {
 
 // DL = D / 64 columns per lane; GM = 4 or 16 heads of register state (G <=
 // GM); F32C: fp32 cache; FUSED: q (and the new k, v) computed from qkv.
-template <int DL, int GM, bool F32C, bool FUSED>
-__global__ void __launch_bounds__(kAttnThreads) attn_kernel(AttnParams a) {
+template <int DL, int GM, bool F32C, bool FUSED, int NWV>
+__global__ void __launch_bounds__(64 * NWV) attn_kernel(AttnParams a) {
+    constexpr int kAttnWaves = NWV;
+    constexpr int kAttnThreads = 64 * NWV;
     constexpr int D = 64 * DL;
     constexpr int T = D / 32;
-    constexpr bool PF = !F32C && DL <= 4;  // prefetch the next block (registers allow it)
+    constexpr bool PF = !F32C && DL <= 4 && NWV == 4;  // prefetch the next block (registers allow it)
     using Blk = KvBlock<DL, F32C>;
     constexpr bool MV = Blk::MV;          // p v on the matrix cores
     constexpr int NT = D / 16;            // its column tiles
@@ -436,12 +436,14 @@ __global__ void __launch_bounds__(kAttnThreads) attn_kernel(AttnParams a) {
     const int64_t mrow = (int64_t)b * a.ld_mask;
 
     // The wave's first block goes out before the prologue's arithmetic --
-    // except in the workgroup whose split holds the new token, which loads
-    // after writing that token's key and value (the barrier at the end of
-    // the prologue orders its own stores before its loads).
+    // except the block that holds the new token, which its wave loads after
+    // the workgroup has written that token's key and value (the barrier at
+    // the end of the prologue orders the workgroup's own stores before its
+    // loads).  Later blocks load after that barrier anyway.
     Blk cur;
     int s0 = s_lo + wave * kBlk;
-    if (!has_new && s0 < s_hi) load_block<DL, F32C>(a, kv_base, s0, s_hi, mrow, lane, cur);
+    const bool first_new = has_new && pos >= s0 && pos < s0 + kBlk;
+    if (!first_new && s0 < s_hi) load_block<DL, F32C>(a, kv_base, s0, s_hi, mrow, lane, cur);
 
     if constexpr (FUSED) {
         // raw rows: [0, G) query heads, G: key head j, G + 1: value head j;
@@ -500,7 +502,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_kernel(AttnParams a) {
     }
     __syncthreads();
 
-    if (has_new && s0 < s_hi) load_block<DL, F32C>(a, kv_base, s0, s_hi, mrow, lane, cur);
+    if (first_new && s0 < s_hi) load_block<DL, F32C>(a, kv_base, s0, s_hi, mrow, lane, cur);
 
     // A operand: row `col` = query head j*G + col (zero rows from G on);
     // element e of step t is scale * q[32t + 8 grp + e], as bf16 hi + lo.
@@ -759,12 +761,18 @@ __global__ void __launch_bounds__(kAttnThreads) attn_kernel(AttnParams a) {
     if (tid == 0) __hip_atomic_store(&a.counters[b * a.HKV + j], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Waves per workgroup: 8 for a bf16 cache with D <= 256 and up to 4 query
+// heads per kv head (one 16-position block per wave at a time, no double
+// buffer, so the blocks of a short context run side by side), else 4 (two
+// blocks in turn per wave on the double-buffered path, or the VALU path).
 template <int DL, int GM, bool FUSED>
 static void launch_attn(const AttnParams& a, bool f32c, dim3 grid, hipStream_t st) {
     if (f32c)
-        hipLaunchKernelGGL((attn_kernel<DL, GM, true, FUSED>), grid, dim3(kAttnThreads), 0, st, a);
+        hipLaunchKernelGGL((attn_kernel<DL, GM, true, FUSED, 4>), grid, dim3(64 * 4), 0, st, a);
+    else if constexpr (DL <= 4 && GM == 4)
+        hipLaunchKernelGGL((attn_kernel<DL, GM, false, FUSED, 8>), grid, dim3(64 * 8), 0, st, a);
     else
-        hipLaunchKernelGGL((attn_kernel<DL, GM, false, FUSED>), grid, dim3(kAttnThreads), 0, st, a);
+        hipLaunchKernelGGL((attn_kernel<DL, GM, false, FUSED, 4>), grid, dim3(64 * 4), 0, st, a);
 }
 
 template <bool FUSED>
