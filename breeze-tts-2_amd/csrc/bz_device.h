@@ -131,6 +131,11 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 __device__ __forceinline__ u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+// The same with the non-temporal hint, for data read once (weights): it does
+// not displace lines that other workgroups read again (x) from the L2.
+__device__ __forceinline__ u32x4 ldg16_nt(const void* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
 
 // Range-checked 16-byte loads through a buffer resource (V#) covering
 // [p, p + bytes): an offset at or past `bytes` returns zeros and sends no

@@ -250,13 +250,13 @@ __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
             if (tile_tiled(WF)) {
                 // the tile of unit u in the 16-row block of column ct (uniform), its scales after the tiles
                 const uint8_t* blk = p.w + (int64_t)(ct >> 4) * tp.chunk;
-                buf[d][t] = ldg16(blk + (int64_t)u * 1024 + loff[t]);
+                buf[d][t] = ldg16_nt(blk + (int64_t)u * 1024 + loff[t]);
                 if (tile_i4(WF))
                     scb[d][t] = *reinterpret_cast<const uint32_t*>(blk + (int64_t)tp.NU * 1024 + u * 64 + j * 4);
                 continue;
             }
             const uint8_t* base = p.w + (int64_t)ct * p.row_bytes + (int64_t)u * 64;  // uniform
-            buf[d][t] = ldg16(base + loff[t]);
+            buf[d][t] = ldg16_nt(base + loff[t]);
             if (WF == WF_I4ZP) {
                 scb[d][t] = (reinterpret_cast<const uint32_t*>(p.sc0) + (int64_t)g * p.N)[soff[t]];
             } else if (WF == WF_I4MIN) {
@@ -269,9 +269,10 @@ __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
     if (active) pipeline_prime<0, D>(nu, 1, nu, 0, ic, issue);
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. stage x (the rest of the slice is loaded here, behind the weights).
-    //    m < M is uniform over each aligned 16-lane group for int4 (nblk is
-    //    a multiple of 16), as the unit sums need.
+    // 2. stage x (the rest of the slice is loaded here, behind the weights,
+    //    kTileXB blocks per thread in flight).  m < M is uniform over each
+    //    aligned 16-lane group for int4 (nblk is a multiple of 16), as the
+    //    unit sums need.
     {
         int m = m_first, kq = kq_first;
 #pragma unroll
@@ -279,7 +280,19 @@ __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
             if (m < M) tile_stage<WF>(xr[i], m, kq, xs, x128, xrow, RS);
             advance(m, kq);
         }
-        for (; m < M; advance(m, kq)) tile_stage<WF>(ldg16(xb + m * ldx + kq * 8), m, kq, xs, x128, xrow, RS);
+        while (m < M) {
+            int mi[kTileXB], ki[kTileXB];
+#pragma unroll
+            for (int i = 0; i < kTileXB; ++i) {
+                mi[i] = m;
+                ki[i] = kq;
+                xr[i] = ldg16(xb + min(m, M - 1) * ldx + kq * 8);
+                advance(m, kq);
+            }
+#pragma unroll
+            for (int i = 0; i < kTileXB; ++i)
+                if (mi[i] < M) tile_stage<WF>(xr[i], mi[i], ki[i], xs, x128, xrow, RS);
+        }
     }
     __syncthreads();
 
@@ -408,8 +421,9 @@ __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
     // The sum over slices, in slice order.  Threads with 8 or more outputs
     // (M = 32 of a 128-column block over 512 threads) take 8 outputs x 4
     // slices of loads per batch, which halves the memory round trips of
-    // 4 x 4; fewer outputs keep 4 x 4, since unused (clamped) loads of the
-    // wider batch still cost requests.
+    // 4 x 4; fewer outputs keep 4 x 4, since unused (clamped) loads of a
+    // wider batch still cost requests (8 x 8 measured 0.8 us slower at M = 32
+    // over 10 slices).
     const int CBW = NW * 16 * T;  // columns of a block (a power of two)
     const int nout = M * CBW;
     if (nout >= 8 * nthr)
