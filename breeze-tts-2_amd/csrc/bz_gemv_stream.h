@@ -103,8 +103,9 @@ struct StreamParams {
 };
 
 // LDS carve-up (bytes), shared with the host launcher: x rows as bf16 (row
-// stride 2K + 16 bytes), the int4 per-unit sums X [row][unit], the waves'
-// sums of x^2 [wave][row] and the partial dot products [row][column][wave].
+// stride 2K + 16 bytes), the int4 per-unit sums X [row][unit], the sums of x^2
+// of each wave's four 16-lane rows [wave][row][4] and the partial dot
+// products [row][column][wave].
 struct StreamLds {
     int xs, xst, sq, red, total;
 };
@@ -114,7 +115,7 @@ __host__ __device__ inline StreamLds stream_lds(int wf, int M, int K, int NW) {
     L.xs = 0;
     L.xst = align16(M * stream_x_row_bytes(K));
     L.sq = L.xst + align16(tiled_i4(wf) ? M * (K / 128) * 4 : 0);
-    L.red = L.sq + align16(NW * M * 4);
+    L.red = L.sq + align16(NW * M * 16);
     L.total = L.red + align16(M * 16 * 16 * 4);  // 16 wave slots
     return L;
 }
@@ -222,43 +223,38 @@ __global__ void __launch_bounds__(1024) gemv_stream(StreamParams p) {
     // 1. stage the slice while the first tiles are in flight: u = bf16(gamma x)
     //    (or x) per block; int4 blocks are stored [x0 x4 x1 x5 x2 x6 x3 x7] and
     //    their unit's sum X is reduced over the unit's 16 consecutive lanes
-    //    (kb0 is a multiple of 16, so a unit is an aligned 16-lane group)
+    //    (kb0 is a multiple of 16, so a unit is an aligned 16-lane group).
+    //    The sums of x^2 and X come from v_dot2_f32_bf16 on the packed
+    //    values (the products of bf16 values are exact in fp32).
     float ss[MM];
 #pragma unroll
     for (int m = 0; m < MM; ++m) ss[m] = 0.0f;
-    auto stage = [&](u32x4 v, u32x4 g, int m, int kl) {
-        float f[8];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            f[2 * q] = bf16_lo(v[q]);
-            f[2 * q + 1] = bf16_hi(v[q]);
-        }
-        if (p.norm) {
+    constexpr uint32_t kOnes = 0x3F803F80u;  // bf16 (1.0, 1.0)
+    auto stage = [&](u32x4 v, u32x4 g, int m, int kl, bool norm) {
+        u32x4 u = v;
+        if (norm) {
             float s2 = 0.0f;
 #pragma unroll
-            for (int q = 0; q < 8; ++q) s2 += f[q] * f[q];
+            for (int q = 0; q < 4; ++q) s2 = dot2(v[q], v[q], s2);
 #pragma unroll
             for (int mm = 0; mm < MM; ++mm)
                 if (mm == m) ss[mm] += s2;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                f[2 * q] = bf16_to_f32(f32_to_bf16(f[2 * q] * bf16_lo(g[q])));
-                f[2 * q + 1] = bf16_to_f32(f32_to_bf16(f[2 * q + 1] * bf16_hi(g[q])));
-            }
+            for (int q = 0; q < 4; ++q) u[q] = pack_bf16x2(bf16_lo(v[q]) * bf16_lo(g[q]), bf16_hi(v[q]) * bf16_hi(g[q]));
         }
-        u32x4 o;
+        u32x4 o = u;
         if (I4) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) o[q] = pack_bf16x2(f[q], f[q + 4]);
-        } else if (p.norm) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) o[q] = pack_bf16x2(f[2 * q], f[2 * q + 1]);
-        } else {
-            o = v;
+            // (x_q, x_{q+4}) pairs: the low halves of u[0], u[2], the high halves, then u[1], u[3]
+            o[0] = __builtin_amdgcn_perm(u[2], u[0], 0x05040100u);
+            o[1] = __builtin_amdgcn_perm(u[2], u[0], 0x07060302u);
+            o[2] = __builtin_amdgcn_perm(u[3], u[1], 0x05040100u);
+            o[3] = __builtin_amdgcn_perm(u[3], u[1], 0x07060302u);
         }
         if (kl < nkb) *reinterpret_cast<u32x4*>(xs + m * xrow + (kb0 + kl) * 16) = o;
         if (I4) {
-            float cs = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
+            float cs = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) cs = dot2(u[q], kOnes, cs);
             cs = sum16_dpp(cs);
             if (kl < nkb && (kl & 15) == 0) xst[m * NU + (kb0 + kl) / 16] = cs;
         }
@@ -283,16 +279,19 @@ __global__ void __launch_bounds__(1024) gemv_stream(StreamParams p) {
                     }
                     u32x4 gg = g;
                     if (t0 >= NXL && p.norm) gg = ldg16(p.gamma + (kb0 + min(lane + 64 * r, nkb - 1)) * 8);
-                    stage(v, gg, m, lane + 64 * r);
+                    if (p.norm)  // uniform
+                        stage(v, gg, m, lane + 64 * r, true);
+                    else
+                        stage(v, gg, m, lane + 64 * r, false);
                 }
             }
         }
     }
-    if (p.norm) {
+    if (p.norm) {  // per 16-lane row; the epilogue adds the four rows of each wave
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
-            const float t = wave_sum(ss[m]);
-            if (lane == 0 && m < M) sq[wave * M + m] = t;
+            const float t = sum16_dpp(ss[m]);
+            if (j == 0 && m < M) sq[(wave * M + m) * 4 + kq] = t;
         }
     }
     // the wave reads back only what it wrote: LDS operations of one wave
@@ -322,12 +321,12 @@ __global__ void __launch_bounds__(1024) gemv_stream(StreamParams p) {
 #pragma unroll
             for (int d = 0; d < 4; ++d) dv = mfma_bf16(*reinterpret_cast<const u32x4*>(xu + d * 16), bq[d], dv);
             const float s = bf16_lo(sc[q]);
-            const float zp = bf16_hi(sc[q]) - 136.0f * s;
+            const float zp = fmaf(-136.0f, s, bf16_hi(sc[q]));
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 if (r < MM) {
                     const float X = xst[min(4 * kq + r, M - 1) * NU + u];
-                    y[r] += s * dv[r] + zp * X;
+                    y[r] = fmaf(s, dv[r], fmaf(zp, X, y[r]));
                 }
             }
         } else {
@@ -372,7 +371,11 @@ __global__ void __launch_bounds__(1024) gemv_stream(StreamParams p) {
         const bool live = gw < NW;
         float a = live ? rg[gw] : 0.0f;
         float a2 = PAIR && live ? rg[8 * 16 + gw] : 0.0f;
-        float s2 = p.norm && live ? sq[gw * M + m] : 0.0f;
+        float s2 = 0.0f;
+        if (p.norm && live) {
+            const float4 q4 = *reinterpret_cast<const float4*>(sq + (gw * M + m) * 4);
+            s2 = (q4.x + q4.y) + (q4.z + q4.w);
+        }
         a = sum16_dpp(a);
         if (PAIR) a2 = sum16_dpp(a2);
         if (p.norm) s2 = sum16_dpp(s2);
