@@ -98,12 +98,14 @@ template <int WF>
 __device__ __forceinline__ void tile_stage(u32x4 v, int m, int kq, uint16_t* xs, float* x128, int xrow, int rstride) {
     u32x4 o = v;
     if (tile_i4(WF)) {
-        o[0] = (v[0] & 0xFFFFu) | (v[2] << 16);
-        o[1] = (v[0] >> 16) | (v[2] & 0xFFFF0000u);
-        o[2] = (v[1] & 0xFFFFu) | (v[3] << 16);
-        o[3] = (v[1] >> 16) | (v[3] & 0xFFFF0000u);
-        float cs = ((bf16_lo(v[0]) + bf16_hi(v[0])) + (bf16_lo(v[1]) + bf16_hi(v[1]))) +
-                   ((bf16_lo(v[2]) + bf16_hi(v[2])) + (bf16_lo(v[3]) + bf16_hi(v[3])));
+        // (x_q, x_{q+4}) pairs by byte permutes; the block's sum by v_dot2 with (1, 1)
+        o[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
+        o[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
+        o[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
+        o[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
+        float cs = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) cs = dot2(v[q], 0x3F803F80u, cs);
         cs = sum16(cs);
         if ((kq & 15) == 0) x128[(kq >> 4) * rstride + m] = cs;
     }
@@ -333,11 +335,11 @@ __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
                 }
                 const uint32_t e = scb[d][t];
                 const float s = bf16_lo(e);
-                const float zp = bf16_hi(e) - (tile_zp(WF) ? 136.0f : 128.0f) * s;
+                const float zp = fmaf(tile_zp(WF) ? -136.0f : -128.0f, s, bf16_hi(e));
 #pragma unroll
                 for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) acc[t][mb][q] += s * dacc[mb][q] + zp * X[mb][q];
+                    for (int q = 0; q < 4; ++q) acc[t][mb][q] = fmaf(s, dacc[mb][q], fmaf(zp, X[mb][q], acc[t][mb][q]));
             }
         } else if (tile_f8(WF)) {
             u32x4 a0[MB], a1[MB];
@@ -421,9 +423,9 @@ __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
     // The sum over slices, in slice order.  Threads with 8 or more outputs
     // (M = 32 of a 128-column block over 512 threads) take 8 outputs x 4
     // slices of loads per batch, which halves the memory round trips of
-    // 4 x 4; fewer outputs keep 4 x 4, since unused (clamped) loads of a
-    // wider batch still cost requests (8 x 8 measured 0.8 us slower at M = 32
-    // over 10 slices).
+    // 4 x 4; fewer outputs keep 4 x 4.  Wider batches measured slower at
+    // M = 32 (8 x 8 over 10 slices: 0.8 us with clamped loads, 1.8 us with
+    // range-checked buffer loads).
     const int CBW = NW * 16 * T;  // columns of a block (a power of two)
     const int nout = M * CBW;
     if (nout >= 8 * nthr)
