@@ -257,8 +257,11 @@ __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
                     scb[d][t] = *reinterpret_cast<const uint32_t*>(blk + (int64_t)tp.NU * 1024 + u * 64 + j * 4);
                 continue;
             }
+            // row-major rows: plain loads (each wave instruction reads 64 bytes of
+            // 16 rows, and a row's next 64 bytes share the cache line; the
+            // non-temporal hint measured up to 4 us slower at fp8 K2560 N20480)
             const uint8_t* base = p.w + (int64_t)ct * p.row_bytes + (int64_t)u * 64;  // uniform
-            buf[d][t] = ldg16_nt(base + loff[t]);
+            buf[d][t] = ldg16(base + loff[t]);
             if (WF == WF_I4ZP) {
                 scb[d][t] = (reinterpret_cast<const uint32_t*>(p.sc0) + (int64_t)g * p.N)[soff[t]];
             } else if (WF == WF_I4MIN) {
