@@ -158,6 +158,8 @@ def gemv(
         if t is not None:
             _require_gpu(name, t, dev)
     _check_weight(w, wfmt, n, K, group, sc0, sc1)
+    if M == 0:  # no rows: the empty result, nothing launched (the library rejects M = 0)
+        return out
     d = _lib.GemvDesc()
     d.abi_version = _lib.ABI_VERSION
     d.M, d.N, d.K = M, n, K

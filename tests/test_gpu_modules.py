@@ -374,6 +374,25 @@ def test_fp8_linear_any_width():
     assert torch.count_nonzero(mod(x)) == 0
 
 
+@pytest.mark.parametrize("kind", ["int4_tiled", "int4_rowmajor", "fp8"])
+def test_modules_empty_batch(kind):
+    """No tokens in, an empty output of the right shape out, with nothing
+    launched -- as torch's int4 / fp8 matmuls return for an empty batch."""
+    N, K = 64, 256
+    lin, _ = _linear(N, K, 77, "cuda")
+    if kind == "fp8":
+        mod = F8.Fp8Linear(lin)
+    else:
+        mod = I4.Int4Linear(lin, group_size=128)
+        if kind == "int4_rowmajor":
+            mod = I4.Int4Linear(lin, group_size=32)   # group 32 keeps the row-major layout
+    for shape in ((0, K), (2, 0, K)):
+        x = torch.randn(*shape, device=_dev()).to(torch.bfloat16)
+        out = mod(x)
+        assert out.shape == (*shape[:-1], N) and out.dtype == x.dtype
+    torch.cuda.synchronize()
+
+
 def test_rmsnorm_and_silu_mul_kernels():
     M, K = 3, 2560
     _, gamma, x = O.synth(1, K, M, seed=60)
