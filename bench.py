@@ -745,7 +745,7 @@ def config_table(torch, G, dev, log) -> list:
                 nbytes = algo_bytes(bits, N, K, M, norm, epi)
                 roof = nbytes / HBM_PEAK_GBPS / 1e3
                 tflops = 2.0 * M * N * K / us / 1e6
-                launch = tuning.lookup(dev, N, K, wfmt, epi, norm, M) if layout == "rowmajor" else None
+                launch = tuning.lookup(dev, N, K, wfmt, epi, norm, M)
                 rows.append({"config": name, "layout": layout, "M": M, "us": round(us, 2),
                              "gbps": round(nbytes / us / 1e3, 1), "roofline_us": round(roof, 2),
                              "frac": round(roof / us, 3), "tflops": round(tflops, 2),

@@ -348,6 +348,16 @@ def _run_table_entry(key: str, M: int, group: int = 128):
         c = Fp8Case(w)
         out = G.gemv(bf16_tensor(x), c.d_codes, wfmt, N, sc0=c.d_scale, gamma=g, epilogue=epi, residual=res)
         w_eff = c.w_eff
+    elif wfmt in (G.W_INT4_TILED, G.W_INT4_TILED_PAIRED):   # the streaming kernel's entries (path 5)
+        c = Int4Case(w, 128, symmetric=True)
+        buf = G.pack_tiled(G.W_INT4_ZP, c.d_packed, K, wfmt, sc0=c.d_sz)
+        out = G.gemv(bf16_tensor(x), buf, wfmt, N, gamma=g, epilogue=epi, residual=res)
+        w_eff = c.w_zp
+    elif wfmt in (G.W_FP8_TILED, G.W_FP8_TILED_PAIRED):
+        c = Fp8Case(w)
+        buf = G.pack_tiled(G.W_FP8, c.d_codes, K, wfmt, sc0=c.d_scale)
+        out = G.gemv(bf16_tensor(x), buf, wfmt, N, gamma=g, epilogue=epi, residual=res)
+        w_eff = c.w_eff
     else:
         wb = O.f32_to_bf16_bits(w)
         out = G.gemv(bf16_tensor(x), bf16_tensor(wb), wfmt, N, gamma=g, epilogue=epi, residual=res)
