@@ -95,7 +95,7 @@ def _weights(fmt, N, K, dev, tiled=False, paired=False):
     return dict(w=b, wfmt=G.W_BF16), 2 * b.numel()
 
 
-def sweep(budget_mb: int, min_gain: float, log=print) -> dict:
+def sweep(budget_mb: int, min_gain: float, log=print, only: str = "") -> dict:
     dev = torch.device("cuda", torch.cuda.current_device())
     arch = tuning.arch_of(dev)
     table = {}
@@ -103,6 +103,12 @@ def sweep(budget_mb: int, min_gain: float, log=print) -> dict:
     jobs += [(name, fmt, N, K, 0, False, ROW_MS, ROW_CANDIDATES, False) for name, fmt, N, K in ROW_SHAPES]
     jobs += [(name + " tiled", fmt, N, K, epi, norm, (1, 2), TILED_CANDIDATES, True)
              for name, fmt, N, K, epi, norm in TILED_SHAPES]
+    # the several-row shapes in the tiled layout: the tile kernel reads it in place
+    jobs += [(name + " tiled", fmt, N, K, 0, False, ROW_MS, [c for c in ROW_CANDIDATES if c[3] == 4], True)
+             for name, fmt, N, K in ROW_SHAPES]
+    if only:
+        jobs = [j for j in jobs if only in j[0]]
+    swept = []
     for name, fmt, N, K, epi, norm, Ms, candidates, tiled in jobs:
         base, wbytes = _weights(fmt, N, K, dev, tiled, epi == G.EPI_SILU_GATE)
         ncopy = max(2, -(-(budget_mb << 20) // wbytes))
@@ -147,6 +153,7 @@ def sweep(budget_mb: int, min_gain: float, log=print) -> dict:
                 t = timed(cfg)
                 if t < best[0]:
                     best = (t, cfg)
+            swept.append(tuning.table_key(arch, N, K, base["wfmt"], epi, norm, M))
             gain = 1 - best[0] / t_auto
             msg = f"{name:16s} M={M}: rule {t_auto:7.2f} us, best {best[0]:7.2f} us {best[1]} ({100 * gain:+.1f}%)"
             log(msg)
@@ -154,7 +161,7 @@ def sweep(budget_mb: int, min_gain: float, log=print) -> dict:
                 table[tuning.table_key(arch, N, K, base["wfmt"], epi, norm, M)] = list(best[1])
         del copies
         torch.cuda.empty_cache()
-    return {"arch": arch, "table": table}
+    return {"arch": arch, "table": table, "swept": swept}
 
 
 def main(argv=None) -> int:
@@ -162,13 +169,22 @@ def main(argv=None) -> int:
     ap.add_argument("--out", default=None, help="table file (default: the package's tune_<arch>.json)")
     ap.add_argument("--budget-mb", type=int, default=512, help="rotating weight copies per shape")
     ap.add_argument("--min-gain", type=float, default=0.03, help="keep entries at least this much faster")
+    ap.add_argument("--only", default="", help="sweep only the shapes whose name contains this")
+    ap.add_argument("--merge", action="store_true",
+                    help="update the existing table: replace the swept keys' entries, keep the others")
     args = ap.parse_args(argv)
-    res = sweep(args.budget_mb, args.min_gain, log=lambda s: print(s, flush=True))
+    res = sweep(args.budget_mb, args.min_gain, log=lambda s: print(s, flush=True), only=args.only)
     path = args.out or str(tuning.table_path(res["arch"]))
+    table = res["table"]
+    if args.merge:
+        src = tuning.table_path(res["arch"])
+        old = json.loads(src.read_text()) if src.exists() else {}
+        table = {k: v for k, v in old.items() if k not in set(res["swept"])}
+        table.update(res["table"])
     with open(path, "w") as f:
-        json.dump(res["table"], f, indent=1, sort_keys=True)
+        json.dump(table, f, indent=1, sort_keys=True)
         f.write("\n")
-    print(f"{len(res['table'])} entries -> {path}", flush=True)
+    print(f"{len(table)} entries -> {path}", flush=True)
     return 0
 
 
