@@ -39,7 +39,8 @@ def test_committed_table_entries_are_valid_shapes():
         if path == 5:  # the streaming kernel of the tiled formats: only the wave count is read
             assert int(wfmt) in (4, 5, 6, 7) and 1 <= waves <= 16 and depth == 0 and tiles == 0 and len(cfg) == 4
             continue
-        assert int(wfmt) in (0, 1, 2, 3)
+        # row-major formats; path 4 also reads the unpaired tiled ones in place
+        assert int(wfmt) in (0, 1, 2, 3) or (path == 4 and int(wfmt) in (4, 6))
         assert depth in (0, 2, 4, 8, 16) and 0 <= waves <= 8 and tiles >= 0 and path in (1, 2, 3, 4)
         if path == 3:
             assert int(wfmt) in (0, 1)  # int8 matrix-core path is for int4 weights only
