@@ -208,16 +208,23 @@ static int launch_tile(int wf, const TileParams& tp, const TileLaunch& l, hipStr
 }
 
 // Launch shape of the tiled streaming kernel for `rows` rows of x (<= 8).
-// Built-in rule (a sweep of 3-16 waves on MI355X over the decode shapes at
-// M = 1, 2): about 4 units (4 KiB of tiles) per wave for int4 and 6 for fp8
-// (e.g. int4 K2560: 5 waves x 4 units; fp8 K2560: 7 x 6), 8 once a row has 64
-// units or more (int4 K10240: 10 x 8), at most 16 waves.
+// Built-in rule (sweeps of 2-16 waves on MI355X over the decode shapes at
+// M = 1, 2).  With more than 256 row blocks (more workgroups than CUs):
+// about 4 units (4 KiB of tiles) per wave for int4 and 6 for fp8 (int4 K2560:
+// 5 waves x 4 units; fp8 K2560: 7 x 6), 8 once a row has 64 units or more.
+// With at most 256 blocks each CU holds one workgroup, and shorter chains per
+// wave win: 2 units per wave for rows of <= 32 units (hidden 1024-2048
+// projections, int4 K4096), else 4, and from 64 units 5 for int4 (down
+// K10240: 16 waves x 5) but 8 for fp8 (o_proj K4096: 13 x 5 measured
+// 0.4 us slower than 8 x 8 at M = 1).  At most 16 waves.
 static int stream_plan(const bz_gemv_desc* d, int rows, StreamLaunch& l) {
     const int wf = d->wfmt;
     const int NU = tiled_units(wf, d->K);
     int nw = d->cfg_waves;
     if (nw < 0 || nw > kStreamMaxWaves) return BZ_ERR_INVALID_ARG;
-    const int per_wave = NU >= 64 ? 8 : (tiled_i4(wf) ? 4 : 6);
+    const bool few_blocks = d->N / 16 <= 256;
+    const int per_wave = few_blocks ? (NU <= 32 ? 2 : (NU >= 64 ? (tiled_i4(wf) ? 5 : 8) : 4))
+                                    : (NU >= 64 ? 8 : (tiled_i4(wf) ? 4 : 6));
     if (!nw) nw = std::min(kStreamMaxWaves, (NU + per_wave - 1) / per_wave);
     const int need = (NU + nw - 1) / nw;
     int upw = 0;
