@@ -72,6 +72,9 @@ TILED_SHAPES = [s for s in SHAPES if s[1] != "bf16"] + [
     ("C3 down, no epi", "fp8", 2560, 10240, 0, False), ("C5 o, no epi", "int4", 2560, 4096, 0, False),
 ]
 TILED_CANDIDATES = [(0, w, 0, 5) for w in (2, 3, 4, 5, 6, 7, 8, 10, 11, 12, 14, 16)]
+# The panel kernel (several rows over the tiled layout): row blocks per
+# workgroup and wave counts.
+PANEL_CANDIDATES = [(0, w, t, 6) for t in (1, 2, 3, 4, 5) for w in (4, 5, 8, 10, 16) if w <= (16 if t == 1 else 8)]
 
 
 def _weights(fmt, N, K, dev, tiled=False, paired=False):
@@ -104,8 +107,10 @@ def sweep(budget_mb: int, min_gain: float, log=print, only: str = "") -> dict:
     jobs += [(name, fmt, N, K, 0, False, ROW_MS, ROW_CANDIDATES, False) for name, fmt, N, K in ROW_SHAPES]
     jobs += [(name + " tiled", fmt, N, K, epi, norm, (1, 2), TILED_CANDIDATES, True)
              for name, fmt, N, K, epi, norm in TILED_SHAPES]
-    # the several-row shapes in the tiled layout: the tile kernel reads it in place
-    jobs += [(name + " tiled", fmt, N, K, 0, False, ROW_MS, [c for c in ROW_CANDIDATES if c[3] == 4], True)
+    # the several-row shapes in the tiled layout: the tile kernel reads it in
+    # place, and the panel kernel
+    jobs += [(name + " tiled", fmt, N, K, 0, False, ROW_MS,
+              [c for c in ROW_CANDIDATES if c[3] == 4] + PANEL_CANDIDATES, True)
              for name, fmt, N, K in ROW_SHAPES]
     if only:
         jobs = [j for j in jobs if only in j[0]]

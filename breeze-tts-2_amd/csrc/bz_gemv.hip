@@ -1,17 +1,18 @@
 // Host dispatcher of the streaming decode GEMV (C ABI entry bz_gemv).  The
 // kernels are in bz_gemv_kernel.h (dot2 path), bz_gemv_mfma.h (bf16
 // matrix-core path), bz_gemv_i8.h (int8 matrix-core path for int4 weights),
-// bz_gemv_tile.h (several-row tile kernel) and bz_gemv_stream.h (the tiled
-// formats' streaming kernel); their instances live in
-// bz_gemv_{,mfma_,i8_,tile_,stream_}<fmt>.hip.
+// bz_gemv_tile.h (several-row tile kernel), bz_gemv_stream.h (the tiled
+// formats' streaming kernel) and bz_gemv_panel.h (their several-row
+// kernel); their instances live in
+// bz_gemv_{,mfma_,i8_,tile_,stream_,panel_}<fmt>.hip.
 #include <algorithm>
 
-#include "bz_gemv_stream.h"
+#include "bz_gemv_panel.h"
 #include "bz_gemv_tile.h"
 
 namespace bz {
 
-enum { PATH_DOT2 = 1, PATH_MFMA = 2, PATH_I8 = 3, PATH_TILE = 4, PATH_STREAM = 5 };
+enum { PATH_DOT2 = 1, PATH_MFMA = 2, PATH_I8 = 3, PATH_TILE = 4, PATH_STREAM = 5, PATH_PANEL = 6 };
 
 static int launch_wf(int wf, int path, const GemvParams& p, const Launch& l, hipStream_t st) {
     if (path == PATH_I8) {
@@ -56,7 +57,7 @@ static int check_desc(const bz_gemv_desc* d, DescInfo& di) {
     if (epi < BZ_EPI_NONE || epi > BZ_EPI_RESIDUAL) return BZ_ERR_INVALID_ARG;
     if (d->out_dtype != BZ_DT_BF16 && d->out_dtype != BZ_DT_F32) return BZ_ERR_INVALID_ARG;
     if (!d->x || !d->w || !d->out) return BZ_ERR_INVALID_ARG;
-    if (d->cfg_path < 0 || d->cfg_path > PATH_STREAM || d->cfg_slices < 0) return BZ_ERR_INVALID_ARG;
+    if (d->cfg_path < 0 || d->cfg_path > PATH_PANEL || d->cfg_slices < 0) return BZ_ERR_INVALID_ARG;
     if (d->reserved0) return BZ_ERR_INVALID_ARG;
     if (d->n_out2 && !is_tiled(wf)) return BZ_ERR_UNSUPPORTED;  // the second store is a streaming-path feature
     if (is_tiled(wf)) {
@@ -67,9 +68,11 @@ static int check_desc(const bz_gemv_desc* d, DescInfo& di) {
         }
         if (tiled_paired(wf) != (epi == BZ_EPI_SILU_GATE)) return BZ_ERR_UNSUPPORTED;
         // the streaming kernel (path 5), or the several-row tile kernel (path 4)
-        // for unpaired weights without the second store
-        if (d->cfg_path == PATH_TILE) {
+        // or panel kernel (path 6) for unpaired weights without the second
+        // store (the panel kernel also without RMSNorm)
+        if (d->cfg_path == PATH_TILE || d->cfg_path == PATH_PANEL) {
             if (tiled_paired(wf) || d->n_out2) return BZ_ERR_UNSUPPORTED;
+            if (d->cfg_path == PATH_PANEL && d->gamma) return BZ_ERR_UNSUPPORTED;
         } else if (d->cfg_path && d->cfg_path != PATH_STREAM) {
             return BZ_ERR_UNSUPPORTED;
         }
@@ -89,7 +92,7 @@ static int check_desc(const bz_gemv_desc* d, DescInfo& di) {
         di.i4 = tiled_i4(wf);
         return BZ_OK;
     }
-    if (d->cfg_path == PATH_STREAM) return BZ_ERR_UNSUPPORTED;
+    if (d->cfg_path == PATH_STREAM || d->cfg_path == PATH_PANEL) return BZ_ERR_UNSUPPORTED;
     const bool i4 = (wf == BZ_W_INT4_ZP || wf == BZ_W_INT4_MIN);
     if ((i4 || wf == BZ_W_FP8) && !d->sc0) return BZ_ERR_INVALID_ARG;
     if (wf == BZ_W_INT4_MIN && !d->sc1) return BZ_ERR_INVALID_ARG;
@@ -190,9 +193,11 @@ static int tile_plan(const bz_gemv_desc* d, const DescInfo& di, int M, TilePlan&
 // The automatic rule takes the tile kernel from this many rows on.
 constexpr int kTileMinRows = 5;
 
-// (Tiled formats: unpaired weights only, and not with the second store.)
+// (Tiled formats: unpaired weights only, and not with the second store;
+// not where the panel kernel is taken.)
+static bool panel_auto(const bz_gemv_desc* d);
 static bool tile_auto(const bz_gemv_desc* d) {
-    return d->cfg_path == 0 && d->M >= kTileMinRows && !d->n_out2 && !tiled_paired(d->wfmt);
+    return d->cfg_path == 0 && d->M >= kTileMinRows && !d->n_out2 && !tiled_paired(d->wfmt) && !panel_auto(d);
 }
 
 static int launch_tile(int wf, const TileParams& tp, const TileLaunch& l, hipStream_t st) {
@@ -298,6 +303,97 @@ static int gemv_tiled(const bz_gemv_desc* d, const DescInfo& di, hipStream_t st)
     return BZ_OK;
 }
 
+// Row blocks per workgroup of the panel kernel's automatic rule: every
+// workgroup reads all of x for its blocks, so a workgroup takes as many
+// blocks as keep the grid at one workgroup per CU (256), at most 5.
+static int panel_blocks(int nblk) { return std::min(5, std::max(1, (nblk + 255) / 256)); }
+
+// The automatic rule takes the panel kernel for unpaired tiled weights
+// without RMSNorm or the second store (measured on MI355X against the
+// streaming and tile kernels, int4 and fp8, N = 2560-20480, K = 2560-10240,
+// M = 2..32):
+//   * from 5 rows on while the x of one launch is at most 256 KB (M K <=
+//     131072): each workgroup reads all of it from L2, so beyond that the
+//     tile kernel's K slices (x read once per 128 columns) win (K = 10240 at
+//     M = 16 and 32);
+//   * 3-4 rows of fp8 over at least 1280 row blocks (N >= 20480).
+static bool panel_auto(const bz_gemv_desc* d) {
+    if (d->cfg_path || !is_tiled(d->wfmt) || tiled_paired(d->wfmt) || d->gamma || d->n_out2) return false;
+    const int M = d->M, rows = std::min(M, kPanelMaxRows);
+    if (M >= 5) return (int64_t)rows * d->K <= 131072;
+    return M >= 3 && !tiled_i4(d->wfmt) && d->N / 16 >= 1280;
+}
+
+// Launch shape of the panel kernel (bz_gemv_panel.h) for `rows` <= 32 rows
+// of x: T row blocks per workgroup (cfg_tiles: 1 to 5; default by the
+// number of blocks), NW waves (cfg_waves; default about 5 units per wave, at
+// most 16 waves, 8 with several blocks) splitting the units UPW each.
+static int panel_plan(const bz_gemv_desc* d, int rows, PanelLaunch& l) {
+    const int wf = d->wfmt;
+    if (tiled_paired(wf) || d->gamma || d->n_out2) return BZ_ERR_UNSUPPORTED;
+    const int NU = tiled_units(wf, d->K);
+    if (!NU) return BZ_ERR_SHAPE;
+    if ((int64_t)rows * d->ldx * 2 >= (int64_t(1) << 31)) return BZ_ERR_UNSUPPORTED;  // 32-bit x offsets
+    const int nblk = d->N / 16;
+    const int T = d->cfg_tiles ? d->cfg_tiles : panel_blocks(nblk);
+    bool t_ok = false;
+    for (int t : kPanelBlocks) t_ok |= t == T;
+    if (!t_ok) return BZ_ERR_INVALID_ARG;
+    const int maxw = T == 1 ? kPanelMaxWaves : 8;
+    int nw = d->cfg_waves;
+    if (nw < 0 || nw > maxw) return BZ_ERR_INVALID_ARG;
+    if (!nw) nw = std::min(maxw, (NU + 4) / 5);
+    const int need = (NU + nw - 1) / nw;
+    int upw = 0;
+    for (int u : kPanelUpw)
+        if (u >= need) {
+            upw = u;
+            break;
+        }
+    if (!upw) return BZ_ERR_UNSUPPORTED;  // K too long for the waves
+    l.nw = (NU + upw - 1) / upw;          // every wave owns at least one unit
+    l.upw = upw;
+    l.T = T;
+    l.mt = rows > 16 ? 2 : 1;
+    l.grid = (unsigned)((nblk + T - 1) / T);
+    l.lds = (size_t)panel_lds(l.nw, T, l.mt);
+    return l.lds <= (size_t)device_lds_limit() ? BZ_OK : BZ_ERR_UNSUPPORTED;
+}
+
+// The panel kernel over all M rows, kPanelMaxRows per launch.
+static int gemv_panel_rows(const bz_gemv_desc* d, hipStream_t st) {
+    const int M = d->M;
+    const int rows = std::min(M, kPanelMaxRows);
+    PanelLaunch l{}, l_rem{};
+    int rc = panel_plan(d, rows, l);
+    if (rc != BZ_OK) return rc;
+    if (M > rows && M % rows && (rc = panel_plan(d, M % rows, l_rem)) != BZ_OK) return rc;
+    PanelParams p;
+    p.ldx = d->ldx;
+    p.w = static_cast<const uint8_t*>(d->w);
+    p.NU = tiled_units(d->wfmt, d->K);
+    p.chunk = tiled_chunk_bytes(d->wfmt, p.NU);
+    p.ldr = d->ldr;
+    p.ldo = d->ldo;
+    p.K = d->K;
+    p.nblk = d->N / 16;
+    p.epi = d->epilogue;
+    p.out_f32 = d->out_dtype == BZ_DT_F32;
+    p.res_f32 = d->residual_dtype == BZ_DT_F32;
+    const size_t osz = p.out_f32 ? 4 : 2, rsz = p.res_f32 ? 4 : 2;
+    for (int m0 = 0; m0 < M; m0 += rows) {
+        const int r = std::min(rows, M - m0);
+        const PanelLaunch& q = r == rows ? l : l_rem;
+        p.M = r;
+        p.x = static_cast<const uint16_t*>(d->x) + (int64_t)m0 * d->ldx;
+        p.out = static_cast<uint8_t*>(d->out) + (int64_t)m0 * d->ldo * osz;
+        p.res = d->residual ? static_cast<const uint8_t*>(d->residual) + (int64_t)m0 * d->ldr * rsz : nullptr;
+        const int lrc = d->wfmt == WF_I4T ? launch_panel_i4t(p, q, st) : launch_panel_f8t(p, q, st);
+        if (lrc != BZ_OK) return lrc;
+    }
+    return BZ_OK;
+}
+
 }  // namespace bz
 
 using namespace bz;
@@ -319,6 +415,8 @@ extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
     const int n_out = di.n_out, glog2 = di.glog2;
     const int64_t row_bytes = di.row_bytes;
     const bool i4 = di.i4;
+
+    if (d->cfg_path == PATH_PANEL || panel_auto(d)) return gemv_panel_rows(d, static_cast<hipStream_t>(stream));
 
     // several-row tile kernel (forced, or automatic from kTileMinRows rows on
     // when the caller passed the workspace it needs): kTileMaxRows rows per

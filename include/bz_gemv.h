@@ -119,8 +119,9 @@ typedef enum bz_dtype {
  * for int4 weights, group >= 128 and K % 128 == 0, x held as two int8
  * planes per row (about 16 significant bits), up to 16 rows per launch;
  * 4 = several-row bf16 MFMA tile kernel, see below; 5 = the streaming
- * kernel of the tiled formats, which always take it: there cfg_waves alone
- * is read, 1..16 waves per row block).
+ * kernel of the tiled formats: there cfg_waves alone is read, 1..16 waves
+ * per row block; 6 = the several-row panel kernel of the tiled formats, see
+ * below).
  * Used by tuning sweeps.
  *
  * Several rows (path 4).  Up to 32 rows of x per launch stream every weight
@@ -136,6 +137,17 @@ typedef enum bz_dtype {
  * share a workspace must not run concurrently.  The automatic rule takes
  * this path from M = 5 on when `workspace` is large enough (or none is
  * needed), else it keeps the row-sliced paths.
+ *
+ * Several rows over the tiled formats (path 6, the panel kernel).  Up to 32
+ * rows of x per launch against an unpaired tiled int4 or fp8 weight
+ * (BZ_W_INT4_TILED, BZ_W_FP8_TILED), no RMSNorm, epilogue NONE or RESIDUAL,
+ * no second store: each workgroup of cfg_waves waves (0: about 5 units per
+ * wave; at most 16, or 8 with several blocks) covers the whole K of
+ * cfg_tiles consecutive 16-row blocks (1..5; 0: enough to keep about 256
+ * workgroups), so it needs no workspace; larger M runs 32 rows per launch.
+ * The automatic rule takes it for these weights from M = 5 on while
+ * min(M, 32) * K <= 131072, and for fp8 at M = 3-4 with N >= 20480; the
+ * tile kernel (when `workspace` allows) or the streaming kernel otherwise.
  */
 typedef struct bz_gemv_desc {
     int32_t abi_version;      /* must be BZ_ABI_VERSION */

@@ -117,11 +117,19 @@ def _desc(L, **kw):
         ({"wfmt": 4, "K": 192, "ldx": 192}, "ERR_SHAPE"),      # int4 unit = 128 k
         ({"wfmt": 4, "group": 64}, "ERR_SHAPE"),               # tiled int4 is group 128
         ({"wfmt": 6, "K": 160, "ldx": 160}, "ERR_SHAPE"),      # fp8 unit = 64 k
-        ({"wfmt": 4, "cfg_path": 2}, "ERR_UNSUPPORTED"),       # tiled formats run paths 4 and 5 only
+        ({"wfmt": 4, "cfg_path": 2}, "ERR_UNSUPPORTED"),       # tiled formats run paths 4, 5 and 6 only
         ({"wfmt": 5, "epilogue": 1, "cfg_path": 4}, "ERR_UNSUPPORTED"),  # paired: streaming path only
         ({"wfmt": 4, "cfg_path": 4, "n_out2": 8, "out2": 1 << 20, "ldo2": 8}, "ERR_UNSUPPORTED"),  # no second store
         ({"cfg_path": 5}, "ERR_UNSUPPORTED"),                  # path 5 reads tiled formats only
-        ({"cfg_path": 6}, "ERR_INVALID_ARG"),
+        ({"cfg_path": 6}, "ERR_UNSUPPORTED"),                  # path 6 reads tiled formats only
+        ({"cfg_path": 7}, "ERR_INVALID_ARG"),
+        ({"wfmt": 4, "cfg_path": 6, "gamma": 1 << 20}, "ERR_UNSUPPORTED"),          # panel: no RMSNorm
+        ({"wfmt": 5, "epilogue": 1, "cfg_path": 6}, "ERR_UNSUPPORTED"),            # ... no paired weights
+        ({"wfmt": 4, "cfg_path": 6, "n_out2": 8, "out2": 1 << 20, "ldo2": 8}, "ERR_UNSUPPORTED"),  # ... no 2nd store
+        ({"wfmt": 4, "cfg_path": 6, "cfg_tiles": 6}, "ERR_INVALID_ARG"),           # ... 1-5 blocks
+        ({"wfmt": 4, "cfg_path": 6, "cfg_waves": 17}, "ERR_INVALID_ARG"),          # ... <= 16 waves
+        ({"wfmt": 4, "cfg_path": 6, "cfg_tiles": 2, "cfg_waves": 9}, "ERR_INVALID_ARG"),  # ... 8 with blocks
+        ({"wfmt": 6, "K": 704, "ldx": 704, "cfg_path": 6, "cfg_waves": 1}, "ERR_UNSUPPORTED"),  # 11 units a wave
         ({"reserved0": 1}, "ERR_INVALID_ARG"),
         ({"n_out2": 8, "out2": 1 << 20, "ldo2": 8}, "ERR_UNSUPPORTED"),            # second store: tiled only
         ({"wfmt": 4, "n_out2": 8, "ldo2": 8}, "ERR_INVALID_ARG"),                # ... needs out2
@@ -221,7 +229,15 @@ def test_workspace_sizes(L):
 @pytest.mark.parametrize(
     "kw,status",
     [
-        ({"cfg_path": 6}, "ERR_INVALID_ARG"),
+        ({"cfg_path": 6}, "ERR_UNSUPPORTED"),                  # path 6 reads tiled formats only
+        ({"cfg_path": 7}, "ERR_INVALID_ARG"),
+        ({"wfmt": 4, "cfg_path": 6, "gamma": 1 << 20}, "ERR_UNSUPPORTED"),          # panel: no RMSNorm
+        ({"wfmt": 5, "epilogue": 1, "cfg_path": 6}, "ERR_UNSUPPORTED"),            # ... no paired weights
+        ({"wfmt": 4, "cfg_path": 6, "n_out2": 8, "out2": 1 << 20, "ldo2": 8}, "ERR_UNSUPPORTED"),  # ... no 2nd store
+        ({"wfmt": 4, "cfg_path": 6, "cfg_tiles": 6}, "ERR_INVALID_ARG"),           # ... 1-5 blocks
+        ({"wfmt": 4, "cfg_path": 6, "cfg_waves": 17}, "ERR_INVALID_ARG"),          # ... <= 16 waves
+        ({"wfmt": 4, "cfg_path": 6, "cfg_tiles": 2, "cfg_waves": 9}, "ERR_INVALID_ARG"),  # ... 8 with blocks
+        ({"wfmt": 6, "K": 704, "ldx": 704, "cfg_path": 6, "cfg_waves": 1}, "ERR_UNSUPPORTED"),  # 11 units a wave
         ({"reserved0": 1}, "ERR_INVALID_ARG"),
         ({"n_out2": 8, "out2": 1 << 20, "ldo2": 8}, "ERR_UNSUPPORTED"),            # second store: tiled only
         ({"wfmt": 4, "n_out2": 8, "ldo2": 8}, "ERR_INVALID_ARG"),                # ... needs out2

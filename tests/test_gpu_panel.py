@@ -1,0 +1,246 @@
+"""GPU parity of the several-row panel kernel (GEMV path 6: up to 32 rows of x
+against an unpaired tiled int4 / fp8 weight, every workgroup covering the
+whole K of its row blocks, x read straight into the matrix-core operands)
+through the C ABI, against the CPU oracle.
+
+Bars as for the other GEMV paths:
+  * max|out-ref|/max|ref| <= 4e-3 against the float64 dequantize-then-matmul
+    of the same packed weights (bench_gemv.py:30-53; the reference's bar is
+    1e-2), asymmetric int4 (z != 0) included;
+  * one-hot rows of x with dyadic scales are bit-exact: every k of every unit
+    lands on its own weight (pins the cross-lane redistribution of the tile
+    pieces, the x piece offsets, the nibble order and the (s, z) rows);
+  * repeated calls and graph replays are bit-identical (fixed summation
+    order over the waves).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bz_oracle as O
+from tests._util import Fp8Case, Int4Case, bf16_tensor, f32, u8_tensor
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+TIGHT = 4e-3
+PANEL = 6
+
+from breeze_amd import gemv as G  # noqa: E402
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+def _x(m, k, seed):
+    return O.f32_to_bf16_bits(_rng(seed).standard_normal((m, k)).astype(np.float32))
+
+
+def _weight(fmt, n, k, seed, symmetric=False):
+    """(tiled buffer, format, W_eff) of an oracle-quantized N(0, 0.02) weight."""
+    w = (_rng(seed).standard_normal((n, k)) * 0.02).astype(np.float32)
+    if fmt == "int4":
+        c = Int4Case(w, 128, symmetric=symmetric)
+        return G.pack_tiled(G.W_INT4_ZP, c.d_packed, k, G.W_INT4_TILED, sc0=c.d_sz), G.W_INT4_TILED, c.w_zp
+    c = Fp8Case(w)
+    return G.pack_tiled(G.W_FP8, c.d_codes, k, G.W_FP8_TILED, sc0=c.d_scale), G.W_FP8_TILED, c.w_eff
+
+
+def _run(buf, wf, n, x_bits, cfg=(0, 0, 0, PANEL), res_bits=None, out_dtype=torch.bfloat16):
+    epi = G.EPI_RESIDUAL if res_bits is not None else G.EPI_NONE
+    return G.gemv(bf16_tensor(x_bits), buf, wf, n, epilogue=epi, cfg=cfg, out_dtype=out_dtype,
+                  residual=bf16_tensor(res_bits) if res_bits is not None else None)
+
+
+def _ref(x_bits, w_eff, res_bits=None):
+    res = O.bf16_bits_to_f32(res_bits) if res_bits is not None else None
+    return O.gemv_ref(O.bf16_bits_to_f32(x_bits), w_eff, O.EPI_RES if res is not None else O.EPI_NONE, res)
+
+
+# Shapes: 3 blocks, 7 blocks (a partial last workgroup for 2-5 blocks per
+# workgroup), 160 blocks; K = 3 / 10 / 20 int4 units (6 / 20 / 40 fp8 units).
+SHAPES = [(48, 384), (112, 1280), (2560, 2560)]
+
+
+@pytest.mark.parametrize("fmt", ["int4", "fp8"])
+@pytest.mark.parametrize("n,k", SHAPES)
+@pytest.mark.parametrize("m", [1, 3, 16, 17, 32, 40])
+@pytest.mark.parametrize("blocks", [1, 3, 5])
+def test_panel_matches_oracle(fmt, n, k, m, blocks):
+    buf, wf, w_eff = _weight(fmt, n, k, n + k + m, symmetric=(m % 2 == 0))
+    x = _x(m, k, 7 * m + blocks)
+    res = _x(m, n, 11 * m + blocks) if blocks != 3 else None
+    got = _run(buf, wf, n, x, cfg=(0, 0, blocks, PANEL), res_bits=res,
+               out_dtype=torch.float32 if m == 17 else torch.bfloat16)
+    assert O.rel_err(f32(got), _ref(x, w_eff, res)) <= TIGHT
+
+
+@pytest.mark.parametrize("fmt", ["int4", "fp8"])
+@pytest.mark.parametrize("waves,blocks", [(1, 1), (3, 1), (7, 1), (16, 1), (1, 2), (5, 4), (8, 5)])
+def test_panel_forced_waves(fmt, waves, blocks):
+    """Every unit split (a last wave with fewer units reads zeros past the
+    row) gives the oracle's result."""
+    n, k, m = 224, 2560, 24
+    buf, wf, w_eff = _weight(fmt, n, k, 300 + waves)
+    x = _x(m, k, 301)
+    units = k // (128 if fmt == "int4" else 64)
+    if -(-units // waves) > 10:  # more units per wave than the kernel is built for
+        with pytest.raises(RuntimeError, match="status 4"):
+            _run(buf, wf, n, x, cfg=(0, waves, blocks, PANEL))
+        return
+    got = _run(buf, wf, n, x, cfg=(0, waves, blocks, PANEL))
+    assert O.rel_err(f32(got), _ref(x, w_eff)) <= TIGHT
+
+
+def _one_hot_rows(K, m_rows, shift):
+    x = np.zeros((m_rows, K), dtype=np.float32)
+    ks = (np.arange(m_rows) * 37 + shift) % K
+    x[np.arange(m_rows), ks] = 1.0
+    return O.f32_to_bf16_bits(x), ks
+
+
+def test_panel_one_hot_int4_bit_exact():
+    """x row m = e_{k_m}: out[m][n] = (q - 8) s + z of weight n at k_m,
+    exactly (dyadic s and z, integer q), for k_m over every k of every unit."""
+    N, K = 48, 512
+    r = _rng(41)
+    q = r.integers(0, 16, size=(N, K), dtype=np.uint8)
+    s = (2.0 ** r.integers(-6, -2, size=(N, K // 128))).astype(np.float32)
+    z = (r.integers(-8, 9, size=(N, K // 128)) * 2.0 ** -5).astype(np.float32)
+    sz = O.scales_zeros(s, z)
+    buf = G.pack_tiled(G.W_INT4_ZP, u8_tensor(O.pack_nibbles_even_low(q)), K, G.W_INT4_TILED, sc0=bf16_tensor(sz))
+    w_eff = O.dequant_int4_zp(q, sz, 128)
+    seen = set()
+    for shift in range(16):
+        x, ks = _one_hot_rows(K, 32, shift * 32)
+        got = f32(_run(buf, G.W_INT4_TILED, N, x, out_dtype=torch.float32))
+        assert np.array_equal(got, w_eff[:, ks].T), shift
+        seen.update(ks.tolist())
+    assert len(seen) == K
+
+
+def test_panel_one_hot_fp8_bit_exact():
+    N, K = 48, 512
+    r = _rng(42)
+    codes = r.integers(0, 256, size=(N, K), dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x3C  # no NaN codes
+    scale = (2.0 ** r.integers(-4, 2, size=N)).astype(np.float32)
+    buf = G.pack_tiled(G.W_FP8, u8_tensor(codes), K, G.W_FP8_TILED, sc0=torch.from_numpy(scale).cuda())
+    w_eff = O.dequant_fp8(codes, scale)
+    seen = set()
+    for shift in range(16):
+        x, ks = _one_hot_rows(K, 32, shift * 32)
+        got = f32(_run(buf, G.W_FP8_TILED, N, x, out_dtype=torch.float32))
+        assert np.array_equal(got, w_eff[:, ks].T), shift
+        seen.update(ks.tolist())
+    assert len(seen) == K
+
+
+# The several-row configuration's shapes (MTP draft verification + CFG).
+FULL = [("int4", 20480, 2560), ("fp8", 20480, 2560), ("int4", 2560, 10240), ("fp8", 2560, 10240),
+        ("int4", 10240, 2560), ("int4", 6144, 2560)]
+
+
+@pytest.mark.parametrize("fmt,n,k", FULL, ids=[f"{f}-N{n}-K{k}" for f, n, k in FULL])
+@pytest.mark.parametrize("m", [3, 8, 32])
+def test_panel_full_size(fmt, n, k, m):
+    buf, wf, w_eff = _weight(fmt, n, k, 500 + m, symmetric=True)
+    x = _x(m, k, 501 + m)
+    a = _run(buf, wf, n, x)
+    b = _run(buf, wf, n, x)
+    assert torch.equal(a, b)
+    e = O.rel_err(f32(a), _ref(x, w_eff))
+    assert e <= TIGHT, e
+
+
+def test_panel_automatic_choice():
+    """The built-in rule takes the panel kernel (bit-identical to forcing it)
+    from 5 rows on while M K <= 131072, for fp8 at 3-4 rows over >= 1280 row
+    blocks, and not beyond (there the tile kernel runs; same result within
+    the bar)."""
+    from breeze_amd import tuning
+
+    saved = dict(tuning._TABLES)
+    tuning._TABLES.clear()
+    tuning._TABLES[tuning.arch_of(torch.device("cuda"))] = {}  # the built-in rule, not the table
+    try:
+        for fmt, n, k, m, panel in [("int4", 2560, 10240, 8, True), ("int4", 2560, 4096, 32, True),
+                                    ("fp8", 20480, 2560, 3, True), ("int4", 2560, 10240, 16, False),
+                                    ("int4", 20480, 2560, 3, False)]:
+            buf, wf, w_eff = _weight(fmt, n, k, 600 + m)
+            x = _x(m, k, 601)
+            auto = _run(buf, wf, n, x, cfg=(0, 0, 0, 0))
+            forced = _run(buf, wf, n, x)
+            assert torch.equal(auto, forced) == panel, (fmt, n, k, m)
+            assert O.rel_err(f32(auto), _ref(x, w_eff)) <= TIGHT
+    finally:
+        tuning._TABLES.clear()
+        tuning._TABLES.update(saved)
+
+
+def test_panel_graph_replays_match_eager():
+    n, k, m = 1280, 2560, 20
+    buf, wf, _ = _weight("int4", n, k, 700)
+    x = bf16_tensor(_x(m, k, 701))
+    res = bf16_tensor(_x(m, n, 702))
+    out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    call = lambda: G.gemv(x, buf, wf, n, epilogue=G.EPI_RESIDUAL, residual=res, out=out, cfg=(0, 0, 0, PANEL))
+    call()
+    torch.cuda.synchronize()
+    want = out.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side), torch.cuda.graph(g, stream=side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    for i in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), i
+        _ = (x.float() * 2).sum().item()  # eager work between replays
+
+
+@pytest.mark.parametrize("fmt", ["int4", "fp8"])
+def test_panel_fp32_residual_aliasing_out(fmt):
+    n, k, m = 320, 1280, 12
+    buf, wf, w_eff = _weight(fmt, n, k, 800)
+    x = _x(m, k, 801)
+    r = _rng(802).standard_normal((m, n)).astype(np.float32)
+    out = torch.from_numpy(r.copy()).cuda()
+    G.gemv(bf16_tensor(x), buf, wf, n, epilogue=G.EPI_RESIDUAL, residual=out, out=out, cfg=(0, 0, 0, PANEL))
+    ref = O.gemv_ref(O.bf16_bits_to_f32(x), w_eff, O.EPI_RES, r)
+    assert O.rel_err(f32(out), ref) <= TIGHT
+
+
+def test_panel_rejects_what_it_cannot_run():
+    """Path 6 takes unpaired tiled weights without RMSNorm or the second
+    store, 1-5 blocks and at most 16 waves (8 with several blocks)."""
+    n, k, m = 64, 512, 4
+    c = Int4Case((_rng(900).standard_normal((n, k)) * 0.02).astype(np.float32), 128)
+    tp = G.pack_tiled(G.W_INT4_ZP, c.d_packed, k, G.W_INT4_TILED_PAIRED, sc0=c.d_sz)
+    t = G.pack_tiled(G.W_INT4_ZP, c.d_packed, k, G.W_INT4_TILED, sc0=c.d_sz)
+    x = bf16_tensor(_x(m, k, 901))
+    gamma = bf16_tensor(O.f32_to_bf16_bits(np.ones(k, np.float32)))
+    cases = [
+        (dict(w=tp, wfmt=G.W_INT4_TILED_PAIRED, epilogue=G.EPI_SILU_GATE), "status 4"),
+        (dict(w=t, wfmt=G.W_INT4_TILED, gamma=gamma), "status 4"),
+        (dict(w=t, wfmt=G.W_INT4_TILED, out2=torch.zeros(m, 16, device="cuda", dtype=torch.bfloat16)), "status 4"),
+        (dict(w=t, wfmt=G.W_INT4_TILED, cfg=(0, 0, 6, PANEL)), "status 1"),
+        (dict(w=t, wfmt=G.W_INT4_TILED, cfg=(0, 17, 1, PANEL)), "status 1"),
+        (dict(w=t, wfmt=G.W_INT4_TILED, cfg=(0, 9, 2, PANEL)), "status 1"),
+    ]
+    for kw, code in cases:
+        kw = dict(kw)
+        w, wf = kw.pop("w"), kw.pop("wfmt")
+        kw["cfg"] = kw.get("cfg", (0, 0, 0, PANEL))
+        with pytest.raises(RuntimeError, match=code):
+            G.gemv(x, w, wf, n, **kw)
+    # row-major weights have no panel path
+    with pytest.raises(RuntimeError, match="status 4"):
+        G.gemv(x, c.d_packed, G.W_INT4_ZP, n, sc0=c.d_sz, cfg=(0, 0, 0, PANEL))

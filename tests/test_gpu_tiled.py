@@ -372,10 +372,11 @@ def test_gemv_tiled_second_store_paired_f32():
 @pytest.mark.parametrize("fmt", ["int4", "fp8"])
 @pytest.mark.parametrize("m", [5, 8, 9, 16, 17, 32, 40])
 def test_tile_kernel_reads_tiled_formats(fmt, m):
-    """From M = 5 on (no RMSNorm, no SiLU-gate) a tiled weight takes the
-    several-row tile kernel, which reads its tiles in place: the result is
-    bit-identical to the same kernel over the row-major weight (same launch
-    plan, same arithmetic) and within the bar of the oracle."""
+    """The several-row tile kernel (path 4) reads a tiled weight in place: the
+    result is bit-identical to the same kernel over the row-major weight
+    (same launch plan, same arithmetic) and within the bar of the oracle.
+    The automatic choice for this shape (M K <= 131072) is the panel kernel
+    (path 6)."""
     n, k = 2560, 2560
     c = _int4_case(n, k, 950 + m) if fmt == "int4" else _fp8_case(n, k, 960 + m)
     tbuf, tf = _tiled_i4(c, False) if fmt == "int4" else _tiled_f8(c, False)
@@ -392,7 +393,10 @@ def test_tile_kernel_reads_tiled_formats(fmt, m):
         w_eff = c.w_eff
     assert torch.equal(got, want)
     auto = G.gemv(bf16_tensor(x), tbuf, tf, n, epilogue=G.EPI_RESIDUAL, residual=bf16_tensor(res))
-    assert torch.equal(auto, got)   # the automatic choice from M = 5 on
+    panel = G.gemv(bf16_tensor(x), tbuf, tf, n, epilogue=G.EPI_RESIDUAL, residual=bf16_tensor(res),
+                   cfg=(0, 0, 0, 6))
+    assert torch.equal(auto, panel)   # the automatic choice from M = 5 on
+    assert O.rel_err(f32(panel), _ref(x, w_eff, None, O.EPI_RES, res)) <= TIGHT
     assert O.rel_err(f32(got), _ref(x, w_eff, None, O.EPI_RES, res)) <= TIGHT
 
 

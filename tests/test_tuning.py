@@ -36,6 +36,11 @@ def test_committed_table_entries_are_valid_shapes():
         assert len(cfg) in (4, 5)
         depth, waves, tiles, path = cfg[:4]
         # 0 = the built-in choice for that field
+        if path == 6:  # the panel kernel: unpaired tiled weights, no prologue or epilogue but the
+            # residual; waves <= 16 (<= 8 with several blocks), 1-5 row blocks per workgroup
+            assert int(wfmt) in (4, 6) and not int(norm) and int(epi) in (0, 2) and depth == 0
+            assert 1 <= tiles <= 5 and 0 <= waves <= (16 if tiles == 1 else 8) and len(cfg) == 4
+            continue
         if path == 5:  # the streaming kernel of the tiled formats: only the wave count is read
             assert int(wfmt) in (4, 5, 6, 7) and 1 <= waves <= 16 and depth == 0 and tiles == 0 and len(cfg) == 4
             continue
