@@ -111,6 +111,8 @@ PROFILE_CASES = [
     ("int4 qkv K2560 N6144 M1", "int4", "tiled", 6144, 2560, 1, 0, True),
     ("int4 o_proj K4096 N2560 M1", "int4", "tiled", 2560, 4096, 1, 2, False),
     ("int4 C4 K10240 N2560 M32 (row-major, split-K tile)", "int4", "rowmajor", 2560, 10240, 32, 0, False),
+    ("int4 C4 K2560 N20480 M32 (tiled, panel)", "int4", "tiled", 20480, 2560, 32, 0, False),
+    ("fp8 C4 K2560 N20480 M32 (tiled, panel)", "fp8", "tiled", 20480, 2560, 32, 0, False),
 ]
 PROFILE_REPS = 12
 
@@ -407,8 +409,11 @@ TILE_REPS = 20
 
 
 def tile_cases() -> list:
-    return [(name, fmt, N, K, M) for name, fmt, N, K, _, _, _ in CONFIG_SHAPES if name.startswith("C4")
-            for M in (16, 32)]
+    return [(name, fmt, N, K, M, layout) for name, fmt, N, K, _, _, _ in CONFIG_SHAPES if name.startswith("C4")
+            for layout in ("rowmajor", "tiled") for M in (16, 32)]
+
+
+SEVERAL_ROW_KERNELS = ("gemv_tile", "gemv_panel")
 
 
 def profile_tiles(torch, G, dev) -> int:
@@ -417,15 +422,11 @@ def profile_tiles(torch, G, dev) -> int:
     rocprofv3 counter and trace runs; --mfma-summary reads them back."""
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
-    for name, fmt, N, K, M in tile_cases():
+    for name, fmt, N, K, M, layout in tile_cases():
         w = torch.randn(N, K, device=dev, generator=gen) * 0.02
-        if fmt == "int4":
-            p, sc = G.quantize_int4_device(w, GROUP, True, G.W_INT4_ZP)[:2]
-            wfmt = G.W_INT4_ZP
-        else:
-            c, sc = G.quantize_fp8_device(w, 1e-12)
-            p, wfmt = c.view(torch.uint8), G.W_FP8
+        base, wfmt, _ = _weights(torch, G, fmt, N, K, 0, w, layout)
         del w
+        p, sc = base[0], (base[1] if len(base) > 1 else None)
         x = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
         out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
         G.gemv(x, p, wfmt, N, sc0=sc, group=GROUP, out=out)  # sizes the workspace (one extra launch)
@@ -433,7 +434,7 @@ def profile_tiles(torch, G, dev) -> int:
         for _ in range(TILE_REPS):
             G.gemv(x, p, wfmt, N, sc0=sc, group=GROUP, out=out)
         torch.cuda.synchronize()
-        log(f"{name} M={M}: {TILE_REPS + 1} launches")
+        log(f"{name} {layout} M={M}: {TILE_REPS + 1} launches")
     return 0
 
 
@@ -456,31 +457,34 @@ def mfma_summary(trace_dir: str, pmc_dir: str) -> int:
     cases = tile_cases()
 
     def groups(seq):
-        # launches of the tile kernel in launch order, split into the tile_cases() runs
+        # launches of the several-row kernels in launch order, split into the tile_cases() runs
         n = TILE_REPS + 1
         if len(seq) != n * len(cases):
             raise SystemExit(f"{len(seq)} tile dispatches, expected {n * len(cases)}")
         return [seq[i * n + 1:(i + 1) * n] for i in range(len(cases))]
 
+    def several(kname):
+        return any(k in kname for k in SEVERAL_ROW_KERNELS)
+
     tr = sorted((int(r["Dispatch_Id"]), int(r["End_Timestamp"]) - int(r["Start_Timestamp"]), r["Kernel_Name"])
-                for r in rows(trace_dir, "*kernel_trace.csv") if "gemv_tile" in r["Kernel_Name"])
+                for r in rows(trace_dir, "*kernel_trace.csv") if several(r["Kernel_Name"]))
     per = {}
     for r in rows(pmc_dir, "*counter_collection.csv"):
-        if "gemv_tile" not in r["Kernel_Name"]:
+        if not several(r["Kernel_Name"]):
             continue
         per.setdefault(int(r["Dispatch_Id"]), {}).setdefault(r["Counter_Name"], 0.0)
         per[int(r["Dispatch_Id"])][r["Counter_Name"]] += float(r["Counter_Value"])
     pm = [per[k] for k in sorted(per)]
     print(f"matrix-core use of the several-row tile GEMVs, MI355X ({MI355X_SIMDS} SIMDs, "
           f"{MI355X_CLOCK_GHZ} GHz peak engine clock); median of {TILE_REPS} launches each")
-    print(f"{'config':28s} {'M':>3s} {'us':>7s} {'TFLOP/s':>8s} {'MFMA busy':>10s} {'util':>7s} "
+    print(f"{'config':28s} {'layout':8s} {'M':>3s} {'us':>7s} {'TFLOP/s':>8s} {'MFMA busy':>10s} {'util':>7s} "
           f"{'MFMA instr':>10s} {'VALU instr':>11s}  kernel")
-    for (name, fmt, N, K, M), t, c in zip(cases, groups(tr), groups(pm)):
+    for (name, fmt, N, K, M, layout), t, c in zip(cases, groups(tr), groups(pm)):
         us = statistics.median(d for _, d, _ in t) / 1e3
         busy = statistics.median(x.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) for x in c)
         util = busy / (MI355X_SIMDS * us * 1e-6 * MI355X_CLOCK_GHZ * 1e9)
-        kern = re.search(r"gemv_tile<[^>]*>", t[0][2])
-        print(f"{name:28s} {M:3d} {us:7.2f} {2.0 * M * N * K / us / 1e6:8.1f} {busy:10.0f} {100 * util:6.2f}% "
+        kern = re.search(r"gemv_(tile|panel)<[^>]*>", t[0][2])
+        print(f"{name:28s} {layout:8s} {M:3d} {us:7.2f} {2.0 * M * N * K / us / 1e6:8.1f} {busy:10.0f} {100 * util:6.2f}% "
               f"{statistics.median(x.get('SQ_INSTS_MFMA', 0.0) for x in c):10.0f} "
               f"{statistics.median(x.get('SQ_INSTS_VALU', 0.0) for x in c):11.0f}  {kern.group(0) if kern else ''}")
     return 0
@@ -708,9 +712,10 @@ def _weights(torch, G, fmt, N, K, epi, w, layout):
 def config_table(torch, G, dev, log) -> list:
     """Each GEMV of C1-C4 (synthetic weights N(0, 0.02), int4 symmetric g128
     or fp8 e4m3 per-row, bf16 x N(0, 1)) in both layouts -- "tiled" (the
-    decode layout the modules hold, streaming kernel, slices of <= 8 rows)
-    and "rowmajor" (the other kernels: row-sliced paths, and the several-row
-    tile kernel from M = 5) -- timed as HIP-graph replays over weight copies
+    decode layout the modules hold: the streaming kernel, and for several
+    rows the panel or tile kernel) and "rowmajor" (the other kernels:
+    row-sliced paths, and the several-row tile kernel from M = 5) -- timed
+    as HIP-graph replays over weight copies
     rotating through >= 1 GiB: µs per call, algorithmic GB/s and the fraction
     of the 8 TB/s bytes-moved roofline."""
     from breeze_amd import tuning
