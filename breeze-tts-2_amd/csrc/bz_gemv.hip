@@ -308,19 +308,25 @@ static int gemv_tiled(const bz_gemv_desc* d, const DescInfo& di, hipStream_t st)
 // blocks as keep the grid at one workgroup per CU (256), at most 5.
 static int panel_blocks(int nblk) { return std::min(5, std::max(1, (nblk + 255) / 256)); }
 
-// The automatic rule takes the panel kernel for unpaired tiled weights
-// without RMSNorm or the second store (measured on MI355X against the
-// streaming and tile kernels, int4 and fp8, N = 2560-20480, K = 2560-10240,
-// M = 2..32):
-//   * from 5 rows on while the x of one launch is at most 256 KB (M K <=
-//     131072): each workgroup reads all of it from L2, so beyond that the
+// Descriptors the panel kernel can run: unpaired tiled weights without
+// RMSNorm or the second store.
+static bool panel_ok(const bz_gemv_desc* d) {
+    return is_tiled(d->wfmt) && !tiled_paired(d->wfmt) && !d->gamma && !d->n_out2;
+}
+
+// The automatic rule takes the panel kernel for them (measured on MI355X
+// against the streaming and tile kernels, int4 and fp8, N = 2560-20480,
+// K = 2560-10240, M = 2..32):
+//   * from 5 rows on while the x of one launch is at most 384 KB (M K <=
+//     196608): each workgroup reads all of it from L2, so beyond that the
 //     tile kernel's K slices (x read once per 128 columns) win (K = 10240 at
-//     M = 16 and 32);
+//     M = 32); without the workspace the tile kernel needs, the panel kernel
+//     at any M >= 5;
 //   * 3-4 rows of fp8 over at least 1280 row blocks (N >= 20480).
 static bool panel_auto(const bz_gemv_desc* d) {
-    if (d->cfg_path || !is_tiled(d->wfmt) || tiled_paired(d->wfmt) || d->gamma || d->n_out2) return false;
+    if (d->cfg_path || !panel_ok(d)) return false;
     const int M = d->M, rows = std::min(M, kPanelMaxRows);
-    if (M >= 5) return (int64_t)rows * d->K <= 131072;
+    if (M >= 5) return (int64_t)rows * d->K <= 196608;
     return M >= 3 && !tiled_i4(d->wfmt) && d->N / 16 >= 1280;
 }
 
@@ -488,6 +494,10 @@ extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
             return BZ_OK;
         }
     }
+    // several rows of a tiled weight the tile kernel did not take (no
+    // workspace): the panel kernel, which needs none
+    if (tiled && d->cfg_path == 0 && M >= kTileMinRows && panel_ok(d))
+        return gemv_panel_rows(d, static_cast<hipStream_t>(stream));
     if (tiled) return gemv_tiled(d, di, static_cast<hipStream_t>(stream));
 
     const bool silu = epi == BZ_EPI_SILU_GATE;

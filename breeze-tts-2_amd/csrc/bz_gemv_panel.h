@@ -15,11 +15,15 @@
 //     units, UPW consecutive units each, and every wave runs its units over
 //     all T blocks (split-K inside the workgroup, summed in a fixed order:
 //     deterministic).
-//   * x never goes through LDS: the 16-byte pieces of x a lane multiplies
-//     are exactly an MFMA operand (below), so each wave loads them from
-//     global memory (L2) straight into registers, once per unit for all T
-//     blocks, with range-checked buffer loads (rows >= M and units past the
-//     block read as zeros and send no request).
+//   * x never goes through LDS memory: each wave loads the 16-byte pieces
+//     of x its MFMAs multiply from global memory (L2) straight into
+//     registers, once per unit for all T blocks, with range-checked buffer
+//     loads (rows >= M and units past the block read as zeros and send no
+//     request).  A load instruction reads 16 rows x 64 bytes; the four
+//     lanes of a quad read one row's 64-byte run (lane 4 a + b: row a, piece
+//     b), and ds_bpermute moves each piece to its MFMA lane a + 16 b (with
+//     the MFMA lane order, a quad would touch four rows: measured 1.5x
+//     slower at M = 32, K = 10240).
 //   * Each wave keeps D units in flight (x pieces, T tiles and, for int4,
 //     T scale quads per unit) in a rolling register pipeline.
 //   * One workgroup barrier: the waves' partials go to LDS, then each thread
@@ -124,15 +128,25 @@ __global__ void __launch_bounds__(T == 1 ? 1024 : 512) gemv_panel(PanelParams p)
     // keeps one offset per row half; rows >= M take an offset past every
     // range (reads as zeros, no request), as does every lane of a unit past
     // the row (empty range).
-    const int kx = I4 ? 8 * kq : 16 * (kq & 1) + 8 * (kq >> 1);
+    // (loaded by quads: lane 4 a + b reads row a's piece b, then ds_bpermute
+    // moves it to lane a + 16 b, the MFMA placement)
+    const int qa = lane >> 2, qb = lane & 3;
+    const int kx = I4 ? 8 * qb : 16 * (qb & 1) + 8 * (qb >> 1);
     const uint32_t xbytes = (uint32_t)(((int64_t)(M - 1) * p.ldx + p.K) * 2);
     constexpr uint32_t kXOob = 0x80000000u;
     uint32_t xlo[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-        const int m = 16 * mt + j;
+        const int m = 16 * mt + qa;
         xlo[mt] = m < M ? (uint32_t)(((int64_t)m * p.ldx + kx) * 2) : kXOob;
     }
+    const int xsrc = ((lane & 15) * 4 + (lane >> 4)) * 4;
+    auto xmove = [&](u32x4 v) -> u32x4 {
+        u32x4 r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = (uint32_t)__builtin_amdgcn_ds_bpermute(xsrc, (int)v[i]);
+        return r;
+    };
     // the workgroup's blocks: tiles and (int4) scale quads; a block past the
     // weight has empty ranges (zeros, no requests) and is never stored, and
     // a unit past the row is past the ranges
@@ -188,7 +202,7 @@ __global__ void __launch_bounds__(T == 1 ? 1024 : 512) gemv_panel(PanelParams p)
                 xs[mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
-                    const u32x4 v = xv[q][mt][d];
+                    const u32x4 v = xmove(xv[q][mt][d]);
                     xp[mt][d][0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
                     xp[mt][d][1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
                     xp[mt][d][2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
@@ -247,8 +261,8 @@ __global__ void __launch_bounds__(T == 1 ? 1024 : 512) gemv_panel(PanelParams p)
             u32x4 x0[MT], x1[MT];
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                x0[mt] = xv[q][mt][0];
-                x1[mt] = xv[q][mt][1];
+                x0[mt] = xmove(xv[q][mt][0]);
+                x1[mt] = xmove(xv[q][mt][1]);
             }
             // the next unit's loads go out here, after this unit's registers
             // are consumed: the scheduler may not hoist them (holding two

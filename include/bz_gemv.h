@@ -146,8 +146,9 @@ typedef enum bz_dtype {
  * cfg_tiles consecutive 16-row blocks (1..5; 0: enough to keep about 256
  * workgroups), so it needs no workspace; larger M runs 32 rows per launch.
  * The automatic rule takes it for these weights from M = 5 on while
- * min(M, 32) * K <= 131072, and for fp8 at M = 3-4 with N >= 20480; the
- * tile kernel (when `workspace` allows) or the streaming kernel otherwise.
+ * min(M, 32) * K <= 196608 (beyond that the tile kernel, or the panel
+ * kernel when `workspace` is too small for the tile kernel), and for fp8 at
+ * M = 3-4 with N >= 20480; the streaming kernel otherwise.
  */
 typedef struct bz_gemv_desc {
     int32_t abi_version;      /* must be BZ_ABI_VERSION */

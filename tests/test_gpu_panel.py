@@ -159,7 +159,7 @@ def test_panel_full_size(fmt, n, k, m):
 
 def test_panel_automatic_choice():
     """The built-in rule takes the panel kernel (bit-identical to forcing it)
-    from 5 rows on while M K <= 131072, for fp8 at 3-4 rows over >= 1280 row
+    from 5 rows on while M K <= 196608, for fp8 at 3-4 rows over >= 1280 row
     blocks, and not beyond (there the tile kernel runs; same result within
     the bar)."""
     from breeze_amd import tuning
@@ -168,8 +168,8 @@ def test_panel_automatic_choice():
     tuning._TABLES.clear()
     tuning._TABLES[tuning.arch_of(torch.device("cuda"))] = {}  # the built-in rule, not the table
     try:
-        for fmt, n, k, m, panel in [("int4", 2560, 10240, 8, True), ("int4", 2560, 4096, 32, True),
-                                    ("fp8", 20480, 2560, 3, True), ("int4", 2560, 10240, 16, False),
+        for fmt, n, k, m, panel in [("int4", 2560, 10240, 16, True), ("int4", 2560, 4096, 32, True),
+                                    ("fp8", 20480, 2560, 3, True), ("int4", 2560, 10240, 32, False),
                                     ("int4", 20480, 2560, 3, False)]:
             buf, wf, w_eff = _weight(fmt, n, k, 600 + m)
             x = _x(m, k, 601)
@@ -244,3 +244,29 @@ def test_panel_rejects_what_it_cannot_run():
     # row-major weights have no panel path
     with pytest.raises(RuntimeError, match="status 4"):
         G.gemv(x, c.d_packed, G.W_INT4_ZP, n, sc0=c.d_sz, cfg=(0, 0, 0, PANEL))
+
+
+def test_panel_taken_without_a_workspace():
+    """Through the C ABI with no workspace, several rows that the rule gives
+    the tile kernel (K10240 at M = 32, which needs split-K partials) run on
+    the panel kernel instead: bit-identical to forcing path 6."""
+    import ctypes
+
+    from breeze_amd import _lib
+
+    n, k, m = 2560, 10240, 32
+    buf, wf, w_eff = _weight("int4", n, k, 1000)
+    x = bf16_tensor(_x(m, k, 1001))
+    out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    d = _lib.GemvDesc()
+    d.abi_version = _lib.ABI_VERSION
+    d.M, d.N, d.K, d.group, d.wfmt = m, n, k, 128, wf
+    d.epilogue, d.out_dtype, d.residual_dtype = G.EPI_NONE, _lib.DT_BF16, _lib.DT_BF16
+    d.eps = 1e-6
+    d.x, d.ldx, d.w = x.data_ptr(), x.stride(0), buf.data_ptr()
+    d.out, d.ldo = out.data_ptr(), out.stride(0)
+    assert _lib.lib().bz_gemv_workspace(ctypes.byref(d)) > 0  # the rule's tile kernel would need one
+    _lib.check(_lib.lib().bz_gemv(ctypes.byref(d), _lib.stream_of(x)), "bz_gemv")
+    want = G.gemv(x, buf, wf, n, cfg=(0, 0, 0, PANEL))
+    assert torch.equal(out, want)
+    assert O.rel_err(f32(out), _ref(_x(m, k, 1001), w_eff)) <= TIGHT
