@@ -167,4 +167,20 @@ __device__ __forceinline__ uint32_t buffer_ld4(__amdgpu_buffer_rsrc_t r, uint32_
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
+// Lane placement of 16-byte pieces.  A wave instruction whose lane 4 a + b
+// reads piece b of row a (a = 0..15, b = 0..3: each quad of lanes reads one
+// row's 64 contiguous bytes) is moved by quad_to_mfma to lane a + 16 b, the
+// placement of the bf16 MFMA operands (row = lane % 16).  `src` is
+// quad_source(lane), computed once.  (Measured on MI355X: it pays for x
+// rows far apart in memory, whose quads would otherwise touch four lines;
+// not for the 1 KiB weight tiles of the streaming kernel, whose quads span
+// two lines: int4 decode GEMVs 1% slower with it.)
+__device__ __forceinline__ int quad_source(int lane) { return ((lane & 15) * 4 + (lane >> 4)) * 4; }
+__device__ __forceinline__ u32x4 quad_to_mfma(u32x4 v, int src) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)v[i]);
+    return r;
+}
+
 }  // namespace bz

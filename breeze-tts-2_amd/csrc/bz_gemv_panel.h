@@ -140,13 +140,8 @@ __global__ void __launch_bounds__(T == 1 ? 1024 : 512) gemv_panel(PanelParams p)
         const int m = 16 * mt + qa;
         xlo[mt] = m < M ? (uint32_t)(((int64_t)m * p.ldx + kx) * 2) : kXOob;
     }
-    const int xsrc = ((lane & 15) * 4 + (lane >> 4)) * 4;
-    auto xmove = [&](u32x4 v) -> u32x4 {
-        u32x4 r;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) r[i] = (uint32_t)__builtin_amdgcn_ds_bpermute(xsrc, (int)v[i]);
-        return r;
-    };
+    const int xsrc = quad_source(lane);
+    auto xmove = [&](u32x4 v) -> u32x4 { return quad_to_mfma(v, xsrc); };
     // the workgroup's blocks: tiles and (int4) scale quads; a block past the
     // weight has empty ranges (zeros, no requests) and is never stored, and
     // a unit past the row is past the ranges
