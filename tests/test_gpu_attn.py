@@ -131,6 +131,16 @@ def test_attn_decode_shapes(HQ, HKV, D, pos, split):
     _attn_check(HQ, HKV, D, 512, pos, split)
 
 
+@pytest.mark.parametrize("HQ,HKV,D", [(16, 4, 256), (8, 2, 128), (4, 2, 128), (8, 8, 64), (16, 16, 64)])
+@pytest.mark.parametrize("S,pos", [(1, 0), (16, 0), (16, 15), (17, 16), (17, 9), (32, 31), (32, 16), (33, 32)])
+@pytest.mark.parametrize("split", [1, 3])
+def test_attn_decode_short_cache(HQ, HKV, D, S, pos, split):
+    """Caches of at most 33 positions (the depth decoder's hold 17): one or
+    two 16-position blocks, the rest of the workgroup's waves idle until the
+    merge."""
+    _attn_check(HQ, HKV, D, S, pos, split, seed=S + pos)
+
+
 @pytest.mark.parametrize("cache_dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("mask_kind", ["add_bf16", "add_f32", "bool", "bcast"])
 def test_attn_decode_dtypes_and_masks(cache_dtype, mask_kind):
@@ -186,7 +196,8 @@ def test_attn_position_outside_cache():
 
 
 @pytest.mark.parametrize("HQ,HKV,D", [(16, 4, 256), (8, 2, 128), (16, 1, 64), (4, 1, 512)])
-@pytest.mark.parametrize("pos,S,split", [(0, 64, 1), (37, 64, 1), (37, 64, 4), (511, 512, None), (300, 512, 16)])
+@pytest.mark.parametrize("pos,S,split", [(0, 64, 1), (37, 64, 1), (37, 64, 4), (511, 512, None), (300, 512, 16),
+                                         (0, 17, 1), (16, 17, 1), (31, 32, 2)])
 @pytest.mark.parametrize("qk_norm", [True, False])
 def test_attention_step_fused_matches_oracle_and_unfused(HQ, HKV, D, pos, S, split, qk_norm):
     """One launch of bz_attn_step against the oracle's rope + cache write +
