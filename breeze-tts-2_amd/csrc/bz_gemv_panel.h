@@ -121,15 +121,15 @@ __global__ void __launch_bounds__(T == 1 ? 1024 : 512) gemv_panel(PanelParams p)
     const int blk0 = blockIdx.x * T;
     const int u0 = wave * UPW;
 
-    // x pieces: row m = 16 mt + j, k = u UK + 32 d + (int4: 8 kq; fp8:
-    // 16 (kq & 1) + 8 (kq >> 1)): the four lanes of a row read one aligned
-    // 64-byte run per instruction.  Each unit's loads go through a buffer
-    // resource starting at the unit (uniform: scalar registers), so a lane
-    // keeps one offset per row half; rows >= M take an offset past every
-    // range (reads as zeros, no request), as does every lane of a unit past
-    // the row (empty range).
-    // (loaded by quads: lane 4 a + b reads row a's piece b, then ds_bpermute
-    // moves it to lane a + 16 b, the MFMA placement)
+    // x pieces: MFMA lane j + 16 kq multiplies row m = 16 mt + j at
+    // k = u UK + 32 d + (int4: 8 kq; fp8: 16 (kq & 1) + 8 (kq >> 1)), so the
+    // four pieces of a row in one instruction are one aligned 64-byte run.
+    // They are loaded by quads (lane 4 a + b reads row a's piece b: one
+    // quad, one run) and moved to the MFMA lane a + 16 b with ds_bpermute.
+    // Each unit's loads go through a buffer resource starting at the unit
+    // (uniform: scalar registers), so a lane keeps one offset per row half;
+    // rows >= M take an offset past every range (reads as zeros, no
+    // request), as does every lane of a unit past the row (empty range).
     const int qa = lane >> 2, qb = lane & 3;
     const int kx = I4 ? 8 * qb : 16 * (qb & 1) + 8 * (qb >> 1);
     const uint32_t xbytes = (uint32_t)(((int64_t)(M - 1) * p.ldx + p.K) * 2);
