@@ -96,6 +96,21 @@ def test_noalloc_matches_bz_gemv_on_shrinking_calls(fmt):
     assert needs[0] > needs[1] > 0 and needs[2] == 0
 
 
+def test_noalloc_tiled_several_rows():
+    """A tiled weight at M = 12 then 5 (the panel kernel, no workspace) and
+    at M = 32 over K10240 (the split-K tile kernel, with the scratch):
+    bz_gemv's result bit for bit."""
+    for n, k, ms in ((2560, 2560, (12, 5)), (2560, 10240, (32,))):
+        w, sc, w_eff = _int4(n, k, 7)
+        t = G.pack_tiled(G.W_INT4_ZP, w, k, G.W_INT4_TILED, sc0=sc)
+        for m in ms:
+            x = _x(m, k, 20 + m)
+            ref, got, need = _both(x, t, G.W_INT4_TILED, n)
+            assert torch.equal(got, ref), (k, m)
+            assert (need > 0) == (k == 10240), (k, m, need)
+            assert O.rel_err(f32(got), O.gemv_ref(x.float().cpu().numpy(), w_eff)) <= 1e-2, (k, m)
+
+
 def test_noalloc_forced_slices_with_residual():
     """Forced tile path with 4 K slices over K2560 N4096: no epilogue at
     M = 8 then 5, a residual epilogue at M = 12 then 7."""
