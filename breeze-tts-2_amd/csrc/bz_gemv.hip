@@ -288,6 +288,7 @@ static int gemv_tiled(const bz_gemv_desc* d, const DescInfo& di, hipStream_t st)
     p.out_f32 = d->out_dtype == BZ_DT_F32;
     p.res_f32 = d->residual_dtype == BZ_DT_F32;
     p.norm = d->gamma != nullptr;
+    p.x_lead = p.NU >= 80 && d->N / 16 <= 256;
     const size_t osz = p.out_f32 ? 4 : 2, rsz = p.res_f32 ? 4 : 2;
     for (int m0 = 0; m0 < M; m0 += rows) {
         const int r = std::min(rows, M - m0);

@@ -100,6 +100,7 @@ struct StreamParams {
     float eps;
     int M, K, NU, n_out;
     int epi, out_f32, res_f32, norm;
+    int x_lead;     // 1: the x loads get a head start before the first tiles (long rows)
 };
 
 // LDS carve-up (bytes), shared with the host launcher: x rows as bf16 (row
@@ -216,6 +217,15 @@ __global__ void __launch_bounds__(1024) gemv_stream(StreamParams p) {
     }
     u32x4 wv[UPW];
     auto issue = [&](int q) { wv[q] = buffer_ld16_nt(wrs, (uint32_t)(u0 + q) * 1024u + j * 64 + kq * 16); };
+    // Long rows (80 units or more) over at most 256 row blocks (at most one
+    // workgroup per CU): the x loads get about 270 ns before the first tiles
+    // go out, so they do not queue behind the tiles of every wave of the CU.
+    // Measured on MI355X: int4 K10240 N2560 5.60 -> 5.32 us, fp8 K10240
+    // N2560 7.53 -> 7.40 us; shorter rows are slower with it (fp8 K4096
+    // N2560, 64 units, 3.96 -> 4.17 us; K2560 N20480 7.30 -> 7.55 us).
+    __builtin_amdgcn_sched_barrier(0);
+    if (p.x_lead) __builtin_amdgcn_s_sleep(10);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int q = 0; q < D; ++q) issue(q);
     __builtin_amdgcn_sched_barrier(0);

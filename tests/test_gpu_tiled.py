@@ -375,7 +375,7 @@ def test_tile_kernel_reads_tiled_formats(fmt, m):
     """The several-row tile kernel (path 4) reads a tiled weight in place: the
     result is bit-identical to the same kernel over the row-major weight
     (same launch plan, same arithmetic) and within the bar of the oracle.
-    The automatic choice for this shape (M K <= 131072) is the panel kernel
+    The automatic choice for this shape (min(M, 32) K <= 196608) is the panel kernel
     (path 6)."""
     n, k = 2560, 2560
     c = _int4_case(n, k, 950 + m) if fmt == "int4" else _fp8_case(n, k, 960 + m)
