@@ -557,6 +557,13 @@ FLOOR_CHUNKS = [
     ("fp8 down K10240 N2560, 160 blocks", 26234880, 163968),
     ("fp8 down bytes, 640 workgroups", 26234880, 40992),
 ]
+# Whole-K floors of the several-row GEMVs (bz_shared_read): every workgroup
+# reads all of x (bf16, M rows) beside its own weight bytes.
+FLOOR_SHARED = [
+    ("int4 K10240 N2560 M=32, one 16-row block per workgroup", 32 * 10240 * 2, 87040, 160),
+    ("int4 K10240 N2560 M=16, one 16-row block per workgroup", 16 * 10240 * 2, 87040, 160),
+    ("int4 K2560 N20480 M=32, five 16-row blocks per workgroup", 32 * 2560 * 2, 5 * 21760, 256),
+]
 
 
 def floors(torch, G, dev, log) -> dict:
@@ -572,20 +579,27 @@ def floors(torch, G, dev, log) -> dict:
       chunks         the same read with the decode GEMVs' own decomposition
                      (one workgroup per 16-row block of a tiled weight) and
                      with more workgroups, at their byte counts;
+      shared_x       bz_shared_read: each workgroup reads all of x and its
+                     own weight bytes, the floor of a several-row GEMV that
+                     gives every workgroup the whole K (weights rotating
+                     through >= 1 GiB, x the same for every call);
       copy_1gib      torch's device-to-device copy of 1 GiB (read + write)."""
     from breeze_amd.fused.kernels import graph_time_us
 
     sink = torch.zeros(4, dtype=torch.int32, device=dev)
     empty = graph_time_us(lambda: G.stream_read(None, sink), iters=256)
 
-    def timed_read(size, chunk):
+    def timed_read(size, chunk, x=None, workgroups=0):
         ncopy = max(2, -(-(1 << 30) // size))
         pool = torch.randint(0, 1 << 30, (ncopy * size // 4,), dtype=torch.int32, device=dev)
         bufs = [pool[i * size // 4:(i + 1) * size // 4] for i in range(ncopy)]
         st = {"i": 0}
 
         def fn():
-            G.stream_read(bufs[st["i"] % ncopy], sink, chunk=chunk)
+            if x is None:
+                G.stream_read(bufs[st["i"] % ncopy], sink, chunk=chunk)
+            else:
+                G.shared_read(x, bufs[st["i"] % ncopy], chunk, workgroups, sink)
             st["i"] += 1
 
         us = graph_time_us(fn, iters=min(2 * ncopy, 256))
@@ -604,6 +618,15 @@ def floors(torch, G, dev, log) -> dict:
         chunks.append({"what": label, "bytes": size, "chunk": chunk, "workgroups": size // chunk, "us": round(us, 3),
                        "gbps": round(size / us / 1e3, 1)})
         log(f"read {label} ({size // chunk} x {chunk} B): {us:.2f} us ({size / us / 1e3:.0f} GB/s)")
+    shared = []
+    for label, xbytes, wchunk, wgs in FLOOR_SHARED:
+        x = torch.randint(0, 1 << 30, (xbytes // 4,), dtype=torch.int32, device=dev)
+        us = timed_read(wchunk * wgs, wchunk, x=x, workgroups=wgs)
+        per_wg = xbytes + wchunk
+        shared.append({"what": label, "x_bytes": xbytes, "w_bytes_per_workgroup": wchunk, "workgroups": wgs,
+                       "us": round(us, 3), "gbps_per_workgroup": round(per_wg / us / 1e3, 1)})
+        log(f"shared-x read {label} ({wgs} x ({xbytes} + {wchunk}) B): {us:.2f} us")
+        del x
     xs = [r["bytes"] for r in reads]
     ys = [r["us"] for r in reads]
     xm, ym = sum(xs) / len(xs), sum(ys) / len(ys)
@@ -627,6 +650,7 @@ def floors(torch, G, dev, log) -> dict:
         f"1 GiB copy {copy_us:.0f} us ({2 * (1 << 30) / copy_us / 1e3:.0f} GB/s read+write)")
     return {"empty_node_us": round(empty, 3), "read": reads,
             "read_fit": {"fixed_us": round(fixed, 3), "gbps": round(1 / slope / 1e3, 1)}, "chunks": chunks,
+            "shared_x": shared,
             "copy_1gib": {"us": round(copy_us, 1), "gbps_read_plus_write": round(2 * (1 << 30) / copy_us / 1e3, 1)}}
 
 

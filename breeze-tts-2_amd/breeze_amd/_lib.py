@@ -49,6 +49,7 @@ EXPORTS = (
     "bz_attn_default_split",
     "bz_sample_cfg",
     "bz_stream_read",
+    "bz_shared_read",
 )
 
 
@@ -140,6 +141,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.bz_attn_default_split.argtypes = [i32]
     lib.bz_stream_read.restype = ctypes.c_int
     lib.bz_stream_read.argtypes = [vp, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_uint32, vp, vp]
+    lib.bz_shared_read.restype = ctypes.c_int
+    lib.bz_shared_read.argtypes = [vp, ctypes.c_size_t, vp, ctypes.c_size_t, i32, ctypes.c_uint32, vp, vp]
     lib.bz_sample_cfg.restype = ctypes.c_int
     lib.bz_sample_cfg.argtypes = [vp, i64, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
 

@@ -374,6 +374,23 @@ def stream_read(buf: Optional[torch.Tensor], sink: torch.Tensor, chunk: int = 16
                "bz_stream_read")
 
 
+def shared_read(x: torch.Tensor, w: Optional[torch.Tensor], wchunk: int, workgroups: int, sink: torch.Tensor,
+                key: int = 0x9E3779B9) -> None:
+    """Launch the whole-K read floor: ``workgroups`` workgroups each read all
+    of ``x`` and their own ``wchunk`` bytes of ``w`` (workgroup b at byte
+    b * wchunk; ``w`` must hold workgroups * wchunk bytes).  ``sink`` as for
+    stream_read."""
+    _require_gpu("sink", sink, sink.device)
+    for name, t in (("x", x), ("w", w)):
+        if t is not None and not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    wbytes = 0 if w is None else w.numel() * w.element_size()
+    if wbytes < workgroups * wchunk:
+        raise ValueError(f"w holds {wbytes} bytes, {workgroups} x {wchunk} needed")
+    _lib.check(_lib.lib().bz_shared_read(x.data_ptr(), x.numel() * x.element_size(), _ptr(w), wchunk, workgroups,
+                                         key, sink.data_ptr(), _lib.stream_of(sink)), "bz_shared_read")
+
+
 # ---- glue kernels ------------------------------------------------------------
 
 

@@ -210,6 +210,16 @@ int bz_gemv(const bz_gemv_desc* d, void* stream);
  * fixed cost of a launch). */
 int bz_stream_read(const void* p, size_t bytes, size_t chunk, uint32_t key, uint32_t* sink, void* stream);
 
+/* Measurement aid, no counterpart in the reference: `workgroups` workgroups
+ * of 1024 threads each read all `xbytes` of `x` (the same bytes for every
+ * workgroup; at most 64 MiB) and their own `wchunk` bytes of `w` (workgroup
+ * b at w + b * wchunk; at most 16 MiB), 16-byte aligned sizes and pointers,
+ * and write nothing unless a thread's XOR equals `key`.  Its duration is the
+ * floor of a several-row GEMV whose workgroups each cover the whole K (every
+ * one streams all of x from L2 beside its weights). */
+int bz_shared_read(const void* x, size_t xbytes, const void* w, size_t wchunk, int workgroups, uint32_t key,
+                   uint32_t* sink, void* stream);
+
 /* Size of bz_gemv_noalloc's static device workspace, per GPU. */
 #define BZ_GEMV_SCRATCH_BYTES ((size_t)8 << 20)
 

@@ -468,3 +468,21 @@ def test_stream_read_validation(L):
     assert lib.bz_stream_read(fake, 4096, 1000, 0, fake, None) == L.ERR_SHAPE           # bytes % chunk
     assert lib.bz_stream_read(fake, 4104, 1368, 0, fake, None) == L.ERR_SHAPE           # chunk % 16
     assert lib.bz_stream_read(fake + 8, 4096, 1024, 0, fake, None) == L.ERR_ALIGNMENT
+
+
+def test_shared_read_validation(L):
+    """The whole-K read floor's argument checks (no launch happens)."""
+    lib = L.lib()
+    fake = 1 << 20
+    assert lib.bz_shared_read(fake, 4096, fake, 1024, 4, 0, None, None) == L.ERR_INVALID_ARG   # no sink
+    assert lib.bz_shared_read(None, 4096, fake, 1024, 4, 0, fake, None) == L.ERR_INVALID_ARG   # no x
+    assert lib.bz_shared_read(fake, 4096, None, 1024, 4, 0, fake, None) == L.ERR_INVALID_ARG   # chunk, no w
+    assert lib.bz_shared_read(fake, 4096, fake, 1024, 0, 0, fake, None) == L.ERR_INVALID_ARG   # no workgroups
+    assert lib.bz_shared_read(fake, 0, fake, 1024, 4, 0, fake, None) == L.ERR_SHAPE            # no x bytes
+    assert lib.bz_shared_read(fake, 4100, fake, 1024, 4, 0, fake, None) == L.ERR_SHAPE         # x % 16
+    assert lib.bz_shared_read(fake, 4096, fake, 1000, 4, 0, fake, None) == L.ERR_SHAPE         # chunk % 16
+    assert lib.bz_shared_read(fake, (64 << 20) + 16, fake, 0, 4, 0, fake, None) == L.ERR_SHAPE
+    assert lib.bz_shared_read(fake, 4096, fake, (16 << 20) + 16, 4, 0, fake, None) == L.ERR_SHAPE
+    assert lib.bz_shared_read(fake + 8, 4096, fake, 1024, 4, 0, fake, None) == L.ERR_ALIGNMENT
+    assert lib.bz_shared_read(fake, 4096, fake + 8, 1024, 4, 0, fake, None) == L.ERR_ALIGNMENT
+    assert lib.bz_shared_read(fake, 4096, fake, 1024, 65537, 0, fake, None) == L.ERR_UNSUPPORTED

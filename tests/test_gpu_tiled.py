@@ -448,3 +448,25 @@ def test_stream_read_writes_only_on_key_match():
     G.stream_read(buf, sink, chunk=16384 * 10, key=0)
     torch.cuda.synchronize()
     assert sink.tolist() == [0, 7, 7, 7]
+
+
+def test_shared_read_reads_x_and_own_chunk():
+    """The whole-K read floor: every workgroup reads all of x (40960 bytes,
+    not a whole number of its rounds) and workgroup b reads w's chunk b: a
+    word planted near the end of x and one in workgroup 3's chunk each reach
+    a thread's XOR."""
+    x = torch.zeros(40960 // 4, dtype=torch.int32, device="cuda")
+    w = torch.zeros(4 * 8192 // 4, dtype=torch.int32, device="cuda")
+    x[(40960 - 16 * 7) // 4] = 0x1234
+    w[(3 * 8192 + 9 * 16 + 8) // 4] = 0x777      # workgroup 3
+    sink = torch.full((4,), 7, dtype=torch.int32, device="cuda")
+    G.shared_read(x, w, 8192, 4, sink, key=0x999)
+    torch.cuda.synchronize()
+    assert sink.tolist() == [7, 7, 7, 7]
+    for key in (0x1234, 0x777, 0):
+        sink.fill_(7)
+        G.shared_read(x, w, 8192, 4, sink, key=key)
+        torch.cuda.synchronize()
+        assert sink.tolist() == [key, 7, 7, 7]
+    with pytest.raises(ValueError):
+        G.shared_read(x, w, 8192, 5, sink)      # w shorter than 5 chunks
