@@ -72,10 +72,14 @@ constexpr int kPanelUpw[] = {1, 2, 3, 4, 5, 6, 8, 10};
 constexpr int kPanelBlocks[] = {1, 2, 3, 4, 5};
 
 // Units in flight per wave: two, or one where a unit's registers are many
-// (int4 with two row halves: 32 VGPRs of x pieces plus their permuted copy;
-// five blocks per workgroup) and a second unit in flight would spill.
+// (int4 with two row halves: 32 VGPRs of x pieces plus their permuted copy)
+// or where a second unit measured slower (several blocks per workgroup with
+// one row half).  fp8 with two row halves and several blocks keeps two:
+// measured on MI355X, K2560 N20480 M = 32 14.1 -> 13.4 us (184 VGPRs, no
+// spills), while two units made int4 K2560 N20480 at M = 8 / 16 and fp8 at
+// M = 16 0.1-1.3 us slower.
 __host__ __device__ constexpr int panel_depth(bool i4, int mt, int t, int upw) {
-    return (t > 1 || (i4 && mt == 2)) ? 1 : (upw <= 2 ? upw : 2);
+    return (i4 ? (t > 1 || mt == 2) : (t > 1 && mt == 1)) ? 1 : (upw <= 2 ? upw : 2);
 }
 
 // LDS: the waves' partials [wave][block][row half][x row % 16][weight row],
