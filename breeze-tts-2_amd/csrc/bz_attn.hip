@@ -285,19 +285,44 @@ __device__ __forceinline__ float vword(const uint32_t (&w)[KvBlock<DL, F32C>::VW
     return (e & 1) ? bf16_hi(w[e >> 1]) : bf16_lo(w[e >> 1]);
 }
 
+// bf16 caches with D = 128 or 256 (the matrix-core p v path) load a block
+// through range-checked buffer loads over the (row, kv head)'s cache, so a
+// wave can issue a block's loads that send no request (an empty range).
+__host__ __device__ constexpr bool kv_buffered(int DL, bool F32C) { return !F32C && DL >= 2 && DL <= 4; }
+
 // One block's loads: key rows s0 + col (lane col), value rows s0 .. s0 + 15
 // and the mask entries, rows past the split's last one clamped to it.  s0
 // and s_hi are wave-uniform, so the value rows' addresses are scalar and
-// each load carries only the lane's column offset.
+// each load carries only the lane's column offset.  On the buffered path a
+// block that is not `live` reads zeros without memory requests (its mask
+// entry still loads, at a clamped position); the other paths always load.
 template <int DL, bool F32C>
 __device__ __forceinline__ void load_block(const AttnParams& a, int64_t kv_base, int s0, int s_hi, int64_t mrow,
-                                           int lane, KvBlock<DL, F32C>& blk) {
+                                           int lane, KvBlock<DL, F32C>& blk, bool live = true) {
     constexpr int D = 64 * DL;
     constexpr int ES = F32C ? 4 : 2;  // element bytes
-    const int last = s_hi - 1;
+    const int last = max(s_hi - 1, 0);  // an empty range reads row 0 (every cache has one), unused
     const int col = lane & 15, grp = lane >> 4;
     const int kpos = min(s0 + col, last);
     blk.mraw = ld_raw(a.mask, a.mask_dtype, mrow + kpos);  // first: its load depends on the dtype
+    if constexpr (kv_buffered(DL, F32C)) {
+        const uint32_t bytes = live ? (uint32_t)a.S * (D * 2) : 0u;  // S D 2 < 2^32 (checked at set-up)
+        const __amdgpu_buffer_rsrc_t kr = buffer_rsrc(static_cast<const char*>(a.kc) + kv_base * 2, bytes);
+        const __amdgpu_buffer_rsrc_t vr = buffer_rsrc(static_cast<const char*>(a.vc) + kv_base * 2, bytes);
+        const uint32_t ko = (uint32_t)kpos * (D * 2) + 16 * grp;
+        for (int t = 0; t < KvBlock<DL, F32C>::T; ++t) {
+            blk.kh[t] = buffer_ld16(kr, ko + 64 * t);
+            blk.kl[t] = u32x4{0u, 0u, 0u, 0u};
+        }
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t vo = (uint32_t)min(s0 + 4 * grp + r, last) * (D * 2) + 8 * DL * col;
+            for (int i = 0; i < DL / 2; ++i) {
+                const u32x4 t = buffer_ld16(vr, vo + 16 * i);
+                for (int e = 0; e < 4; ++e) blk.v[r][4 * i + e] = t[e];
+            }
+        }
+        return;
+    }
     const char* kc = static_cast<const char*>(a.kc) + kv_base * ES;
     const char* krow = kc + (int64_t)kpos * (D * ES) + 8 * grp * ES;
     for (int t = 0; t < KvBlock<DL, F32C>::T; ++t) load_k8<F32C>(krow, 32 * t, blk.kh[t], blk.kl[t]);
@@ -439,11 +464,19 @@ __global__ void __launch_bounds__(64 * NWV) attn_kernel(AttnParams a) {
     // except the block that holds the new token, which its wave loads after
     // the workgroup has written that token's key and value (the barrier at
     // the end of the prologue orders the workgroup's own stores before its
-    // loads).  Later blocks load after that barrier anyway.
+    // loads).  Later blocks load after that barrier anyway.  On the buffered
+    // path every wave issues the block's loads, empty (no requests) where the
+    // wave has no block or holds the new token: with the same loads on every
+    // path, the waits for the query rows below count exactly instead of also
+    // waiting for the cache rows behind a branch.  Measured on MI355X (16 q /
+    // 4 kv heads of 256, bf16 cache of 1024, one row): 9.5 -> 8.6 us at 128
+    // positions, 13.6 -> 12.7 us at 1024 over 8 splits; 0.2-0.3 us slower at
+    // 256-512 positions over 8 splits, where most waves issue empty loads.
     Blk cur;
     int s0 = s_lo + wave * kBlk;
     const bool first_new = has_new && pos >= s0 && pos < s0 + kBlk;
-    if (!first_new && s0 < s_hi) load_block<DL, F32C>(a, kv_base, s0, s_hi, mrow, lane, cur);
+    const bool first_live = !first_new && s0 < s_hi;
+    if (kv_buffered(DL, F32C) || first_live) load_block<DL, F32C>(a, kv_base, s0, s_hi, mrow, lane, cur, first_live);
 
     if constexpr (FUSED) {
         // raw rows: [0, G) query heads, G: key head j, G + 1: value head j;
@@ -804,6 +837,7 @@ static int attn_setup(AttnParams& a, const void* k_cache, const void* v_cache, i
     if ((ld_mask != 0 && ld_mask < S) || ld_mask < 0 || ld_out < (int64_t)HQ * D) return BZ_ERR_SHAPE;
     const int G = HQ / HKV;
     if (D != 64 && D != 128 && D != 256 && D != 512) return BZ_ERR_UNSUPPORTED;
+    if ((int64_t)S * D * 4 >= (int64_t(1) << 32)) return BZ_ERR_UNSUPPORTED;  // 32-bit offsets in one head's cache
     if (G > 16 || (G > 4 && D == 512)) return BZ_ERR_UNSUPPORTED;
     if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(out, 2) || !aligned(workspace, 4))
         return BZ_ERR_ALIGNMENT;
