@@ -391,7 +391,6 @@ __global__ void __launch_bounds__(64 * NWV) attn_kernel(AttnParams a) {
     __shared__ float p_lds[kAttnWaves][kBlk * GM];  // MV: [head][position], else [position][head]
     __shared__ float st_m[kAttnWaves][GM], st_l[kAttnWaves][GM];
     __shared__ float wgt[kAttnWaves][GM], hm[GM], hl[GM];
-    __shared__ float wsp[GM][BZ_ATTN_MAX_SPLIT];
     __shared__ float st_acc[kAttnWaves][GM][D];  // also the raw qkv rows of the prologue
     __shared__ int last;
 
@@ -744,49 +743,55 @@ __global__ void __launch_bounds__(64 * NWV) attn_kernel(AttnParams a) {
     }
     __syncthreads();
     if (!last) return;
-    // Weights first: wave w takes heads w, w + 4, ...; lane s reads split s's
-    // (m, l) and the wave forms w_s = exp(m_s - max m) and sum_s w_s l_s.
-    for (int h = wave; h < G; h += kAttnWaves) {
-        const float* ph = a.part + (hq0 + h) * a.split * (D + 4);
-        const bool in = lane < a.split;
-        const int sl = in ? lane : 0;
-        const float ms0 = __hip_atomic_load(ph + sl * (D + 4) + D, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const float ls0 = __hip_atomic_load(ph + sl * (D + 4) + D + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const float ms = in ? ms0 : kNegBig;
-        const float mt = wave_max(ms);
-        const float w = in ? fexp2((ms - mt) * kLog2e) : 0.0f;
-        wsp[h][lane] = w;
-        const float lt = wave_sum(in ? ls0 * w : 0.0f);
-        if (lane == 0) hl[h] = lt;
-    }
-    __syncthreads();
-    // Then the columns: element i = (h, d) sums w_s acc_s over the splits in
-    // split order; each thread keeps NE elements x 8 splits of loads in flight.
+    // Element i = (h, d): each thread loads, for its NE elements, every
+    // split's partial and its head's (m, l) in batches of SB splits (all in
+    // flight at once; SB NE <= 16 keeps them in registers), and merges them
+    // in split order, online: with M the running max, acc and L are rescaled
+    // by exp(M_old - M) and gain w_s acc_s and w_s l_s, w_s = exp(m_s - M).
+    // One memory round trip per batch and no barrier (the weights were first
+    // formed per head in LDS: a second round trip and a barrier).
     constexpr int NE = (GM * D + kAttnThreads - 1) / kAttnThreads;
-    float acc0[NE];
-    for (int q = 0; q < NE; ++q) acc0[q] = 0.0f;
-    for (int s0 = 0; s0 < a.split; s0 += 8) {
-        float v[NE][8];
+    constexpr int SB = NE <= 2 ? 8 : (NE <= 4 ? 4 : (NE <= 8 ? 2 : 1));
+    float acc0[NE], lsum[NE], mrun[NE];
+    for (int q = 0; q < NE; ++q) {
+        acc0[q] = 0.0f;
+        lsum[q] = 0.0f;
+        mrun[q] = kNegBig;
+    }
+    for (int s0 = 0; s0 < a.split; s0 += SB) {
+        float v[NE][SB], ms[NE][SB], ls[NE][SB];
         for (int q = 0; q < NE; ++q) {
             const int i = min(tid + q * kAttnThreads, G * D - 1);
             const int h = i / D, d = i - h * D;
-            const float* ph = a.part + (hq0 + h) * a.split * (D + 4) + d;
-            for (int u = 0; u < 8; ++u) {
-                const int sidx = min(s0 + u, a.split - 1);
-                v[q][u] = __hip_atomic_load(ph + sidx * (D + 4), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float* ph = a.part + (hq0 + h) * a.split * (D + 4);
+            for (int u = 0; u < SB; ++u) {
+                const float* pp = ph + min(s0 + u, a.split - 1) * (D + 4);
+                v[q][u] = __hip_atomic_load(pp + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ms[q][u] = __hip_atomic_load(pp + D, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ls[q][u] = __hip_atomic_load(pp + D + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
         for (int q = 0; q < NE; ++q) {
-            const int h = min(tid + q * kAttnThreads, G * D - 1) / D;
-            for (int u = 0; u < 8; ++u)
-                if (s0 + u < a.split) acc0[q] += v[q][u] * wsp[h][s0 + u];
+            float mb = mrun[q];
+            for (int u = 0; u < SB; ++u)
+                if (s0 + u < a.split) mb = fmaxf(mb, ms[q][u]);
+            const float rs = fexp2((mrun[q] - mb) * kLog2e);
+            acc0[q] *= rs;
+            lsum[q] *= rs;
+            mrun[q] = mb;
+            for (int u = 0; u < SB; ++u)
+                if (s0 + u < a.split) {
+                    const float w = fexp2((ms[q][u] - mb) * kLog2e);
+                    acc0[q] += v[q][u] * w;
+                    lsum[q] += ls[q][u] * w;
+                }
         }
     }
     for (int q = 0; q < NE; ++q) {
         const int i = tid + q * kAttnThreads;
         if (i < G * D) {
             const int h = i / D, d = i - h * D;
-            const float lt = hl[h];
+            const float lt = lsum[q];
             a.out[(int64_t)b * a.ld_out + (int64_t)(j * G + h) * D + d] =
                 f32_to_bf16(lt > 0.0f ? acc0[q] / lt : 0.0f);
         }
