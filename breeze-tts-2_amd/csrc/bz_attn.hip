@@ -176,7 +176,7 @@ __global__ void __launch_bounds__(kRopeThreads) qkv_rope_cache_kernel(
 // Decode attention: one workgroup per (batch row b, kv head j, split sp).
 // ---------------------------------------------------------------------------
 constexpr int kBlk = 16;           // positions per block (the MFMA's 16 columns)
-constexpr int kUnsplitMax = 192;   // attended positions up to which a call runs unsplit
+constexpr int kUnsplitMax = 160;   // attended positions up to which a call runs unsplit
 constexpr float kNegBig = -1e30f;  // initial running max, as the reference
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -448,9 +448,11 @@ __global__ void __launch_bounds__(64 * NWV) attn_kernel(AttnParams a) {
     const int kv_len = pos < 0 ? 0 : (pos >= a.S ? a.S : (int)pos + 1);
     // Short contexts run unsplit: the workgroup of split 0 takes every
     // position and writes the output itself; the others leave before any
-    // barrier.  Up to about 192 positions that beats a split plus the
-    // cross-workgroup combine (three serialized memory round trips).  The
-    // choice follows the device position, so a captured graph adapts to it.
+    // barrier.  Up to about 160 positions that beats a split plus the
+    // cross-workgroup combine (measured on MI355X, 16 q / 4 kv heads of 256:
+    // unsplit 8.5 against 9.7 us at 128 positions, even at 160, split 9.9
+    // against 10.2 us at 192).  The choice follows the device position, so a
+    // captured graph adapts to it.
     const int nsp = kv_len <= kUnsplitMax ? 1 : a.split;
     if (sp >= nsp) return;
     const int per = (kv_len + nsp - 1) / nsp;

@@ -65,7 +65,7 @@ int bz_qkv_rope_cache(const void* qkv, int64_t ld_qkv, int32_t B, int32_t HQ,
  * ranges; for split > 1 the last workgroup of each (row, kv head) to finish
  * combines the ranges, through `workspace` (bz_attn_workspace bytes, zeroed
  * once before its first use: the kernel leaves its arrival counters at zero
- * again).  While at most 192 positions are attended (decided on the device
+ * again).  While at most 160 positions are attended (decided on the device
  * from *pos) the call runs unsplit whatever `split` says: the workgroup of
  * split 0 covers every position and writes the output, the others return at
  * once and the workspace is not touched.  Calls that share a workspace must

@@ -157,10 +157,10 @@ def test_attn_split_counts_agree(split):
     assert O.rel_err(a, b) <= TIGHT
 
 
-@pytest.mark.parametrize("pos,split", [(191, 8), (192, 8), (193, 64), (250, 64)])
+@pytest.mark.parametrize("pos,split", [(159, 8), (160, 8), (191, 8), (193, 64), (250, 64)])
 def test_attn_unsplit_threshold_and_empty_splits(pos, split):
-    """Around the on-device unsplit threshold (192 attended positions: pos 191
-    runs unsplit, pos 192 splits), and splits left empty above it (64 splits
+    """Around the on-device unsplit threshold (160 attended positions: pos 159
+    runs unsplit, pos 160 splits), and splits left empty above it (64 splits
     over 194 / 251 positions: per = 4, the last splits hold nothing) with the
     cross-workgroup combine: all equal the unsplit result."""
     a = _attn_check(16, 4, 256, 512, pos, split, seed=13)
