@@ -390,7 +390,6 @@ __global__ void __launch_bounds__(64 * NWV) attn_kernel(AttnParams a) {
     __shared__ u32x4 qop[T][2][64];  // the A operand (q hi, lo) of every lane
     __shared__ float p_lds[kAttnWaves][kBlk * GM];  // MV: [head][position], else [position][head]
     __shared__ float st_m[kAttnWaves][GM], st_l[kAttnWaves][GM];
-    __shared__ float wgt[kAttnWaves][GM], hm[GM], hl[GM];
     __shared__ float st_acc[kAttnWaves][GM][D];  // also the raw qkv rows of the prologue
     __shared__ int last;
 
@@ -698,33 +697,26 @@ __global__ void __launch_bounds__(64 * NWV) attn_kernel(AttnParams a) {
     __syncthreads();
 
     // Merge the waves in a fixed order; write the output or the partial.
-    if (tid < G) {
-        const int h = tid;
-        float mt = kNegBig;
-        for (int w = 0; w < kAttnWaves; ++w) mt = fmaxf(mt, st_m[w][h]);
-        float lt = 0.0f;
-        for (int w = 0; w < kAttnWaves; ++w) {
-            const float f = fexp2((st_m[w][h] - mt) * kLog2e);
-            wgt[w][h] = f;
-            lt += st_l[w][h] * f;
-        }
-        hm[h] = mt;
-        hl[h] = lt;
-    }
-    __syncthreads();
+    // Each thread forms its head's wave weights itself (8 values from LDS):
+    // no serial step and no barrier between the state and the merge.
     const int64_t hq0 = (int64_t)b * a.HQ + (int64_t)j * G;
     for (int i = tid; i < G * D; i += kAttnThreads) {
         const int h = i / D, d = i - h * D;
-        float at = 0.0f;
-        for (int w = 0; w < kAttnWaves; ++w) at += st_acc[w][h][d] * wgt[w][h];
-        const float lt = hl[h];
+        float mt = kNegBig;
+        for (int w = 0; w < kAttnWaves; ++w) mt = fmaxf(mt, st_m[w][h]);
+        float lt = 0.0f, at = 0.0f;
+        for (int w = 0; w < kAttnWaves; ++w) {
+            const float f = fexp2((st_m[w][h] - mt) * kLog2e);
+            lt += st_l[w][h] * f;
+            at += st_acc[w][h][d] * f;
+        }
         if (nsp == 1) {
             a.out[(int64_t)b * a.ld_out + (int64_t)(j * G + h) * D + d] = f32_to_bf16(lt > 0.0f ? at / lt : 0.0f);
         } else {  // agent-scope stores: coherent across XCDs without an L2 write-back
             float* pp = a.part + ((hq0 + h) * a.split + sp) * (D + 4);
             __hip_atomic_store(&pp[d], at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (d == 0) {
-                __hip_atomic_store(&pp[D], hm[h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&pp[D], mt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(&pp[D + 1], lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
