@@ -135,7 +135,16 @@ __global__ void __launch_bounds__(T == 1 ? 1024 : 512) gemv_panel(PanelParams p)
     // rows >= M take an offset past every range (reads as zeros, no
     // request), as does every lane of a unit past the row (empty range).
     const int qa = lane >> 2, qb = lane & 3;
-    const int kx = I4 ? 8 * qb : 16 * (qb & 1) + 8 * (qb >> 1);
+    // int4 with two row halves loads each quad's four pieces 64 bytes apart
+    // (x in the tile's own piece order: lane a + 16 g of register d holds
+    // k = 32 g + 8 d of row a), so the weight pieces need no transpose; it
+    // saves 4 permlane swaps per tile and was measured faster only there
+    // (int4 K2560 N20480 M = 32 14.5 -> 14.2 us; with one row half, M = 8 /
+    // 16, about 1 us slower, where each quad reads four 16-byte pieces over
+    // two lines of its row instead of one 64-byte run).
+    constexpr bool XT = I4 && MT == 2;
+    const int kx = I4 ? (XT ? 32 * qb : 8 * qb) : 16 * (qb & 1) + 8 * (qb >> 1);
+    constexpr uint32_t kXStep = XT ? 16u : 64u;  // bytes between a lane's pieces d
     const uint32_t xbytes = (uint32_t)(((int64_t)(M - 1) * p.ldx + p.K) * 2);
     constexpr uint32_t kXOob = 0x80000000u;
     uint32_t xlo[MT];
@@ -170,7 +179,7 @@ __global__ void __launch_bounds__(T == 1 ? 1024 : 512) gemv_panel(PanelParams p)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int d = 0; d < NX; ++d) xv[q][mt][d] = buffer_ld16(xrs, xlo[mt] + 64 * d);
+            for (int d = 0; d < NX; ++d) xv[q][mt][d] = buffer_ld16(xrs, xlo[mt] + kXStep * d);
 #pragma unroll
         for (int t = 0; t < T; ++t) wv[q][t] = buffer_ld16_nt(wrs[t], (uint32_t)u * 1024u + wlane);
         if (I4) {
@@ -224,7 +233,7 @@ __global__ void __launch_bounds__(T == 1 ? 1024 : 512) gemv_panel(PanelParams p)
             // block by block: unpack its tile, 4 MFMAs per row half, scale
 #pragma unroll
             for (int t = 0; t < T; ++t) {
-                const u32x4 v = transpose_pieces(wr[t]);
+                const u32x4 v = XT ? wr[t] : transpose_pieces(wr[t]);
                 u32x4 bq[4];
 #pragma unroll
                 for (int d = 0; d < 4; ++d)
