@@ -271,7 +271,7 @@ static int gemv_tiled(const bz_gemv_desc* d, const DescInfo& di, hipStream_t st)
     if (rc != BZ_OK) return rc;
     StreamLaunch l_rem = l;  // the last, shorter launch (planned before anything is launched)
     if (M > rows && M % rows && stream_plan(d, M % rows, l_rem) != BZ_OK) return BZ_ERR_UNSUPPORTED;
-    StreamParams p;
+    StreamParams p{};
     p.ldx = d->ldx;
     p.w = static_cast<const uint8_t*>(d->w);
     p.chunk = tiled_chunk_bytes(d->wfmt, tiled_units(d->wfmt, d->K));
@@ -375,7 +375,7 @@ static int gemv_panel_rows(const bz_gemv_desc* d, hipStream_t st) {
     int rc = panel_plan(d, rows, l);
     if (rc != BZ_OK) return rc;
     if (M > rows && M % rows && (rc = panel_plan(d, M % rows, l_rem)) != BZ_OK) return rc;
-    PanelParams p;
+    PanelParams p{};
     p.ldx = d->ldx;
     p.w = static_cast<const uint8_t*>(d->w);
     p.NU = tiled_units(d->wfmt, d->K);
@@ -439,7 +439,7 @@ extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
             if (!ws_ok) return BZ_ERR_INVALID_ARG;
         }
         if (trc == BZ_OK && ws_ok) {
-            TileParams tp;
+            TileParams tp{};
             GemvParams& p = tp.p;
             p.w = static_cast<const uint8_t*>(d->w);
             p.row_bytes = row_bytes;
