@@ -280,15 +280,12 @@ __global__ void __launch_bounds__(1024) gemv_stream(StreamParams p) {
             for (int m = 0; m < MM; ++m) {
                 if (m < M) {
                     const int t = t0 + 1 + m;
-                    u32x4 v;
-                    if (t < NXL) {
-                        v = xl[t];
-                    } else {  // beyond the register budget: a plain load now (L2)
-                        const int kl = min(lane + 64 * r, nkb - 1);
-                        v = ldg16(p.x + (int64_t)m * p.ldx + (kb0 + kl) * 8);
-                    }
+                    // beyond the register budget: a load now (L2), range-checked
+                    // like the ones above, so a lane past the slice reads zeros
+                    // and adds nothing to the row's sum of squares
+                    const u32x4 v = t < NXL ? xl[t] : buffer_ld16(xrs, xoff(r, m + 1));
                     u32x4 gg = g;
-                    if (t0 >= NXL && p.norm) gg = ldg16(p.gamma + (kb0 + min(lane + 64 * r, nkb - 1)) * 8);
+                    if (t0 >= NXL && p.norm) gg = buffer_ld16(grs, xoff(r, 0));
                     if (p.norm)  // uniform
                         stage(v, gg, m, lane + 64 * r, true);
                     else

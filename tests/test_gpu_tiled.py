@@ -213,6 +213,44 @@ def test_gemv_tiled_fp8(m, n, k, norm, epi):
     assert O.rel_err(got, rm) <= ONE_BF16_STEP
 
 
+# RMSNorm over slices whose x and gamma loads exceed the kernel's register
+# budget (rounds x (1 + rows) > 12: the later loads are issued during the
+# staging).  Lanes past a wave's slice must read zeros there, or the row's
+# sum of squares counts the slice's last block again (rows 2 and up of the
+# launch then get a wrong 1/rms).  (fmt, n, k, epilogue, rows, cfg)
+NORM_BEYOND_REGISTERS = [
+    ("int4", 2048, 8192, 0, 5, (0, 0, 0, 0)),    # 13 waves x 5 units, 2 rounds
+    ("int4", 2048, 8192, 0, 8, (0, 0, 0, 0)),
+    ("int4", 1024, 10240, 1, 6, (0, 0, 0, 0)),   # paired, 16 waves x 5 units
+    ("fp8", 2048, 10240, 0, 5, (0, 0, 0, 0)),    # 16 waves x 10 units, 2 rounds
+    ("fp8", 2048, 10240, 2, 8, (0, 0, 0, 0)),
+    ("int4", 512, 2560, 0, 6, (0, 4, 0, 5)),     # forced 4 waves x 5 units
+    ("int4", 512, 2560, 0, 4, (0, 2, 0, 5)),     # forced 2 waves x 10 units, 3 rounds
+    ("fp8", 512, 2560, 1, 6, (0, 4, 0, 5)),     # paired, forced 4 waves x 10 units
+]
+
+
+@pytest.mark.parametrize("fmt,n,k,epi,m,cfg", NORM_BEYOND_REGISTERS,
+                         ids=[f"{c[0]}-n{c[1]}-k{c[2]}-e{c[3]}-m{c[4]}-w{c[5][1]}" for c in NORM_BEYOND_REGISTERS])
+def test_gemv_tiled_norm_beyond_register_budget(fmt, n, k, epi, m, cfg):
+    seed = 600 + m + k // 512
+    c = _int4_case(n, k, seed) if fmt == "int4" else _fp8_case(n, k, seed)
+    buf, tf = _tiled_i4(c, epi == 1) if fmt == "int4" else _tiled_f8(c, epi == 1)
+    w_eff = c.w_zp if fmt == "int4" else c.w_eff
+    x_bits = _x(m, k, seed + 1)
+    # rows of very different scale, so a wrong 1/rms of any row shows
+    x_bits = O.f32_to_bf16_bits(O.bf16_bits_to_f32(x_bits) * (1.0 + 3.0 * np.arange(m, dtype=np.float32))[:, None])
+    gamma_bits = _gamma(k, seed + 2)
+    n_out = n // 2 if epi == 1 else n
+    res_bits = _x(m, n_out, seed + 3) if epi == 2 else None
+    out = G.gemv(bf16_tensor(x_bits), buf, tf, n, gamma=bf16_tensor(gamma_bits), epilogue=epi,
+                 residual=bf16_tensor(res_bits) if res_bits is not None else None, cfg=cfg)
+    got = f32(out)
+    ref = _ref(x_bits, w_eff, gamma_bits, epi, res_bits)
+    for r in range(m):  # per row: a row with a wrong norm fails on its own
+        assert O.rel_err(got[r:r + 1], ref[r:r + 1]) <= TIGHT, r
+
+
 @pytest.mark.parametrize("waves", [1, 2, 3, 7, 16])
 def test_gemv_tiled_forced_waves(waves):
     """Every wave count (uneven unit splits, idle waves) gives the same sums;
