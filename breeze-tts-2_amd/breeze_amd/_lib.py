@@ -31,6 +31,7 @@ MASK_BOOL = 2  # include/bz_attn.h
 EXPORTS = (
     "bz_abi_version",
     "bz_strerror",
+    "bz_stream_capture",
     "bz_gemv_workspace",
     "bz_gemv",
     "bz_gemv_noalloc",
@@ -104,6 +105,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.bz_abi_version.argtypes = []
     lib.bz_strerror.restype = ctypes.c_char_p
     lib.bz_strerror.argtypes = [ctypes.c_int]
+    lib.bz_stream_capture.restype = ctypes.c_int
+    lib.bz_stream_capture.argtypes = [vp, ctypes.POINTER(i32), ctypes.POINTER(ctypes.c_uint64)]
     lib.bz_gemv_workspace.restype = ctypes.c_size_t
     lib.bz_gemv_workspace.argtypes = [ctypes.POINTER(GemvDesc)]
     lib.bz_gemv.restype = ctypes.c_int
@@ -180,3 +183,36 @@ def check(status: int, what: str) -> None:
 def stream_of(t: torch.Tensor) -> int:
     """Raw hipStream_t of torch's current stream on t's device."""
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def capture_of(stream: int):
+    """The id of the graph capture under way on the raw HIP stream, or None."""
+    active, cid = ctypes.c_int32(0), ctypes.c_uint64(0)
+    check(lib().bz_stream_capture(stream, ctypes.byref(active), ctypes.byref(cid)), "bz_stream_capture")
+    return cid.value if active.value else None
+
+
+def stream_workspace(table: dict, key: tuple, nbytes: int, device: torch.device, stream: int,
+                     retired: list) -> torch.Tensor:
+    """A zero-filled int32 buffer of at least ``nbytes`` owned by
+    (``key``, stream) -- and, while a graph capture is under way on the
+    stream, by that capture -- so calls on different streams, and different
+    captured graphs, never share one.
+
+    Outside a capture the buffer is allocated and zeroed eagerly on the
+    stream.  Inside a capture it comes from the graph's memory pool and its
+    zero fill (a fill kernel, not a memset node) is recorded into the graph,
+    ahead of the calls that use it, so every replay starts from zeroed
+    counters; the kernels leave them zero again either way.  An outgrown
+    buffer is kept in ``retired`` for the life of the process, since a graph
+    captured earlier may still point at it."""
+    cap = capture_of(stream)
+    full = key + (stream, cap)
+    buf = table.get(full)
+    if buf is None or buf.numel() * 4 < nbytes:
+        n = max(nbytes, 2 * (buf.numel() * 4 if buf is not None else 0), 1 << 20)
+        if buf is not None:
+            retired.append(buf)
+        buf = torch.zeros(-(-n // 4), dtype=torch.int32, device=device)
+        table[full] = buf
+    return buf

@@ -109,23 +109,22 @@ def qkv_rope_cache(qkv, cos, sin, cache_position, keys, values, HQ: int, q_norm_
 
 
 _ATTN_WS: dict[tuple, torch.Tensor] = {}
+_ATTN_WS_RETIRED: list = []
 
 
-def _attn_workspace(B, HQ, HKV, D, split, device) -> Optional[torch.Tensor]:
-    """Split partials and arrival counters, one zeroed buffer per shape and
-    device, allocated on first use (models/fused/kernels.py:480-489).  The
-    kernel leaves the counters at zero, so the buffer is never cleared again
-    (nothing to record in a captured graph); calls that share it must not
-    overlap, as with the reference's cached partial buffer."""
+def _attn_workspace(B, HQ, HKV, D, split, device, stream) -> Optional[torch.Tensor]:
+    """Split partials and arrival counters (models/fused/kernels.py:480-489):
+    one zeroed buffer per shape, device and stream -- and per graph capture
+    while one is under way, with its zero fill recorded into the graph -- so
+    split attention steps on different streams, or in graphs replayed on
+    different streams, never share one (the reference caches one buffer per
+    shape for every stream).  The kernel leaves the counters at zero, so
+    calls on one stream reuse the buffer without clearing it."""
     if split <= 1:
         return None
-    key = (B, HQ, HKV, D, split, str(device))
-    buf = _ATTN_WS.get(key)
-    if buf is None:
-        n = -(-attn_workspace_bytes(B, HQ, HKV, D, split) // 4)
-        buf = torch.zeros(n, device=device, dtype=torch.int32)
-        _ATTN_WS[key] = buf
-    return buf
+    key = (B, HQ, HKV, D, split, device.index if device.index is not None else torch.cuda.current_device())
+    return _lib.stream_workspace(_ATTN_WS, key, attn_workspace_bytes(B, HQ, HKV, D, split), device, stream,
+                                 _ATTN_WS_RETIRED)
 
 
 def _mask_rows(mask: torch.Tensor, B: int, S: int) -> tuple[torch.Tensor, int, int]:
@@ -170,7 +169,7 @@ def attn_decode(q, keys, values, mask, cache_position, out=None, split: Optional
         raise ValueError("q must be a contiguous float32 [B, HQ, D] tensor")
     m2, mcode, ld_mask = _mask_rows(mask, B, S)
     split = default_split(S) if split is None else split
-    ws = _attn_workspace(B, HQ, HKV, D, split, dev)
+    ws = _attn_workspace(B, HQ, HKV, D, split, dev, _lib.stream_of(q))
     out = _out_buffer(out, B, HQ, D, dev)
     _lib.check(
         _lib.lib().bz_attn_decode(
@@ -226,7 +225,7 @@ def attention_step(qkv, cos, sin, cache_position, keys, values, mask, q_norm_w=N
             raise ValueError("seq_len must not alias cache_position")
     m2, mcode, ld_mask = _mask_rows(mask, B, S)
     split = default_split(S) if split is None else split
-    ws = _attn_workspace(B, HQ, HKV, D, split, dev)
+    ws = _attn_workspace(B, HQ, HKV, D, split, dev, _lib.stream_of(qkv))
     out = _out_buffer(out, B, HQ, D, dev)
     _lib.check(
         _lib.lib().bz_attn_step(

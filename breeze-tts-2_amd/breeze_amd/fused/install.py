@@ -1,12 +1,15 @@
 """Install fused decode layers on a model's backbone and depth decoder
-(models/fused/install.py:16-70).
+(models/fused/install.py:16-70: same entry points, keywords and return
+value).
 
-The reference runs one dummy decode step per layer after installing, to tune
-and compile its Triton kernels outside any graph capture.  Nothing here
-tunes (launch shapes come from a static rule in the library), but the step
-is kept: it loads libbzgemv.so, checks every layer's shapes against the
-kernels' limits and leaves the caching allocator warm, before a caller
-captures anything.
+After swapping the layers, each one is readied for graph capture by
+``FusedDecoderLayer.prepare``: its four decode GEMVs run once on zero rows
+of the serving batch, which loads libbzgemv.so (an error if it is missing;
+there is no fallback), makes the library accept every weight at that batch
+and sizes any GEMV workspace on the current stream; and the split-attention
+workspace of the cache length is allocated.  No cache is built and no
+attention runs: nothing here tunes (launch shapes come from a static rule in
+the library), so no per-shape first call has to happen outside a capture.
 """
 
 from __future__ import annotations
@@ -29,39 +32,29 @@ def static_cache(config, max_cache_len: int, batch_size: int):
         return StaticCache(config=config, max_cache_len=max_cache_len)
 
 
-def _install(stack, max_seq: int, batch_size: int, mlp_bits, attn_bits) -> int:
-    n = 0
-    for i, layer in enumerate(stack.layers):
-        if isinstance(layer, FusedDecoderLayer):
-            continue
-        stack.layers[i] = FusedDecoderLayer(layer, i, mlp_bits=mlp_bits, attn_bits=attn_bits)
-        n += 1
-    p = next(stack.parameters())
-    dev, dtype = p.device, p.dtype
-    cache = static_cache(stack.config, max_seq, batch_size)
-    x = torch.zeros(batch_size, 1, stack.config.hidden_size, device=dev, dtype=dtype)
-    mask = torch.zeros(batch_size, 1, 1, max_seq, device=dev, dtype=dtype)
-    pos = torch.zeros(1, dtype=torch.long, device=dev)
-    pos_ids = torch.zeros(batch_size, 1, dtype=torch.long, device=dev)
+def _swap_and_prepare(stack, cache_len: int, batch_size: int, mlp_bits, attn_bits) -> int:
+    """Wrap every layer of ``stack`` not yet fused; prepare all of them for
+    ``batch_size`` rows over a cache of ``cache_len`` positions.  Returns the
+    number of layers wrapped by this call."""
+    fresh = [i for i, layer in enumerate(stack.layers) if not isinstance(layer, FusedDecoderLayer)]
+    for i in fresh:
+        stack.layers[i] = FusedDecoderLayer(stack.layers[i], i, mlp_bits=mlp_bits, attn_bits=attn_bits)
     with torch.no_grad():
-        cos, sin = stack.rotary_emb(x, pos_ids)
         for layer in stack.layers:
-            layer(x, attention_mask=mask, position_ids=pos_ids, past_key_values=cache, use_cache=True,
-                  cache_position=pos, position_embeddings=(cos, sin))
-    del cache
-    torch.cuda.synchronize(dev)
-    return n
+            layer.prepare(batch_size, cache_len)
+    torch.cuda.current_stream().synchronize()
+    return len(fresh)
 
 
 def install_fused_backbone(model, *, batch_size: int = 2, max_seq_len: int = 1024, mlp_bits: int | None = None,
                            attn_bits: int = 16) -> int:
     """Replace every backbone layer by a FusedDecoderLayer; returns how many
     were replaced (models/fused/install.py:16-41)."""
-    return _install(model.backbone_model, max_seq_len, batch_size, mlp_bits, attn_bits)
+    return _swap_and_prepare(model.backbone_model, max_seq_len, batch_size, mlp_bits, attn_bits)
 
 
 def install_fused_depth(model, *, batch_size: int = 2, mlp_bits: int | None = None, attn_bits: int = 16) -> int:
     """Same for the depth decoder, whose cache holds 2 + num_codebooks
     positions (models/fused/install.py:44-70)."""
     dm = model.depth_decoder.model
-    return _install(dm, 2 + dm.config.num_codebooks, batch_size, mlp_bits, attn_bits)
+    return _swap_and_prepare(dm, 2 + dm.config.num_codebooks, batch_size, mlp_bits, attn_bits)

@@ -101,7 +101,47 @@ class FusedDecoderLayer(nn.Module):
             return c
         return None
 
+    # -- set-up before capture -------------------------------------------------
+
+    def prepare(self, rows: int, cache_len: int) -> None:
+        """Run the four decode GEMVs once on ``rows`` zero rows (the library
+        accepts every weight at this batch; any GEMV workspace is sized on
+        the current stream) and allocate the split-attention workspace of a
+        ``cache_len``-position cache, so a decode step can be captured
+        without a first-use allocation of either."""
+        from .. import attention as _attn
+
+        dev = self.ln1.device
+        x = torch.zeros(rows, self.wqkv.K, device=dev, dtype=torch.bfloat16)
+        rms_gemv(x, self.wqkv, self.ln1, self.eps)
+        a = torch.zeros(rows, self.wo.K, device=dev, dtype=torch.bfloat16)
+        h = rms_gemv(a, self.wo, None, epilogue=EPI_RESIDUAL, residual=x)
+        act = rms_gemv(h, self.wgu, self.ln2, self.eps, epilogue=EPI_SILU_GATE)
+        rms_gemv(act, self.wd, None, epilogue=EPI_RESIDUAL, residual=h)
+        hq = (self.wqkv.N - 2 * self.hkv * self.hd) // self.hd
+        split = _attn.default_split(cache_len)
+        if split > 1:
+            _attn._attn_workspace(rows, hq, self.hkv, self.hd, split, dev, torch.cuda.current_stream(dev).cuda_stream)
+
     # -- forward -----------------------------------------------------------------
+
+    def _tokens_in_turn(self, hidden_states, attention_mask, position_ids, past_key_values, use_cache,
+                        cache_position, position_embeddings):
+        """T <= 4 new tokens (the depth decoder's two-position start) as T
+        single-token steps in order: token t attends to the cache through
+        position t, which is what row t of the causal mask allows, so the
+        steps reproduce the original layer's T-token call."""
+        cos, sin = position_embeddings
+
+        def pick(t, tensor, dim):
+            return None if tensor is None else tensor.narrow(dim, t, 1)
+
+        steps = [self.forward(hidden_states.narrow(1, t, 1), attention_mask=attention_mask.narrow(2, t, 1),
+                              position_ids=pick(t, position_ids, 1), past_key_values=past_key_values,
+                              use_cache=use_cache, cache_position=pick(t, cache_position, 0),
+                              position_embeddings=(cos.narrow(1, t, 1), sin.narrow(1, t, 1)))
+                 for t in range(hidden_states.shape[1])]
+        return torch.cat(steps, dim=1)
 
     def forward(self, hidden_states, attention_mask=None, position_ids=None, past_key_values=None,
                 use_cache=False, cache_position=None, position_embeddings=None, **kwargs):
@@ -114,18 +154,8 @@ class FusedDecoderLayer(nn.Module):
                              past_key_values=past_key_values, use_cache=use_cache,
                              position_embeddings=position_embeddings, **kwargs)
         if T > 1:
-            # a short prefill (the depth decoder's 2-position start) is exactly
-            # T causal decode steps: same rope, same mask rows, same cache
-            cos, sin = position_embeddings
-            outs = []
-            for t in range(T):
-                outs.append(self.forward(
-                    hidden_states[:, t: t + 1], attention_mask=attention_mask[:, :, t: t + 1],
-                    position_ids=None if position_ids is None else position_ids[:, t: t + 1],
-                    past_key_values=past_key_values, use_cache=use_cache,
-                    cache_position=None if cache_position is None else cache_position[t: t + 1],
-                    position_embeddings=(cos[:, t: t + 1], sin[:, t: t + 1])))
-            return torch.cat(outs, dim=1)
+            return self._tokens_in_turn(hidden_states, attention_mask, position_ids, past_key_values, use_cache,
+                                        cache_position, position_embeddings)
         x = hidden_states[:, 0]
         layer_cache = self._layer_cache(past_key_values, hidden_states)
         counter = self._counter(layer_cache, x.device)

@@ -187,12 +187,13 @@ def gemv(
     d.out, d.ldo = out.data_ptr(), out.stride(0)
     if out2 is not None:
         d.out2, d.ldo2, d.n_out2 = out2.data_ptr(), out2.stride(0), out2.shape[1]
+    stream = _lib.stream_of(x)
     if M >= _TILE_MIN_ROWS or cfg[3] == _PATH_TILE:
         need = _lib.lib().bz_gemv_workspace(ctypes.byref(d))
         if need:
-            ws = _workspace(dev, need)
+            ws = _workspace(dev, stream, need)
             d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel() * 4
-    _lib.check(_lib.lib().bz_gemv(ctypes.byref(d), _lib.stream_of(x)), "bz_gemv")
+    _lib.check(_lib.lib().bz_gemv(ctypes.byref(d), stream), "bz_gemv")
     return out
 
 
@@ -290,33 +291,21 @@ def pack_tiled(src_wfmt: int, w: torch.Tensor, k: int, dst_wfmt: int, *, sc0: Op
 # counters) that is zero-filled once and left zeroed by every call.
 _TILE_MIN_ROWS = 5
 _PATH_TILE = 4
-_GEMV_WS: dict = {}
+_GEMV_WS: dict = {}          # (device index, raw stream, capture id or None) -> int32 buffer
 _GEMV_WS_RETIRED: list = []  # outgrown workspaces: a captured graph may still point at one
 
 
-def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
-    """The device's GEMV workspace, grown (zero-filled) to at least nbytes.
-    One buffer per device, shared by every call on it: tile-path GEMVs on the
-    same device must not run concurrently on different streams (as with the
-    reference's cached split-K buffer, models/fused/kernels.py:179,192-198).  It
-    must be sized before a graph capture: an eager call of the same shape
-    (the graphs' warm-up steps) does that.  An outgrown buffer is kept alive
-    for the process, since a graph captured earlier still uses it (its
-    counters are zero again once its last call has finished)."""
+def _workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """The GEMV workspace of (device, stream), grown to at least nbytes.
+
+    Each stream has its own, and so has each graph capture (allocated from
+    the graph's pool with its zero fill recorded into the graph), so tile-path
+    GEMVs on different streams, or in graphs replayed on different streams,
+    never share one; the reference keeps one cached split-K buffer per device
+    for every stream (models/fused/kernels.py:179,192-198).  Calls on one
+    stream run in order and may share it."""
     key = dev.index if dev.index is not None else torch.cuda.current_device()
-    buf = _GEMV_WS.get(key)
-    if buf is None or buf.numel() * 4 < nbytes:
-        if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError(
-                f"GEMV workspace of {nbytes} bytes needed inside a graph capture; run the same call once "
-                "eagerly before capturing"
-            )
-        n = max(nbytes, 2 * (buf.numel() * 4 if buf is not None else 0), 1 << 20)
-        if buf is not None:
-            _GEMV_WS_RETIRED.append(buf)
-        buf = torch.zeros(-(-n // 4), dtype=torch.int32, device=torch.device("cuda", key))
-        _GEMV_WS[key] = buf
-    return buf
+    return _lib.stream_workspace(_GEMV_WS, (key,), nbytes, torch.device("cuda", key), stream, _GEMV_WS_RETIRED)
 
 
 # ---- custom-op registration (torch.compile / fake tensors) -----------------

@@ -218,6 +218,16 @@ extern "C" const char* bz_strerror(int status) {
     }
 }
 
+extern "C" int bz_stream_capture(void* stream, int32_t* active, uint64_t* id) {
+    if (!active || !id) return BZ_ERR_INVALID_ARG;
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    unsigned long long cid = 0;
+    if (hipStreamGetCaptureInfo(static_cast<hipStream_t>(stream), &status, &cid) != hipSuccess) return BZ_ERR_LAUNCH;
+    *active = status == hipStreamCaptureStatusActive ? 1 : 0;
+    *id = *active ? (uint64_t)cid : 0;
+    return BZ_OK;
+}
+
 extern "C" int bz_rmsnorm(const void* x, int64_t ldx, const void* gamma, float eps, void* out, int64_t ldo, int32_t M,
                           int32_t K, void* stream) {
     if (!x || !gamma || !out || M < 1 || K < 1 || ldx < K || ldo < K) return BZ_ERR_INVALID_ARG;

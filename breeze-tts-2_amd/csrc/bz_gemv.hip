@@ -134,6 +134,11 @@ static int check_desc(const bz_gemv_desc* d, DescInfo& di) {
     return BZ_OK;
 }
 
+int gemv_check_desc(const bz_gemv_desc* d) {
+    DescInfo di;
+    return check_desc(d, di);
+}
+
 // Launch shape of the several-row tile kernel (bz_gemv_tile.h).
 struct TilePlan {
     int MB, T, D, nw, ks, nsl, ncb;

@@ -68,10 +68,10 @@ int device_scratch(hipStream_t st, uint8_t** out) {
 }  // namespace bz
 
 extern "C" int bz_gemv_noalloc(const bz_gemv_desc* d, void* stream) {
-    if (!d) return BZ_ERR_INVALID_ARG;
-    if (d->abi_version != BZ_ABI_VERSION) return BZ_ERR_ABI;
-    // 0 for calls that need no workspace and for invalid descriptors (which
-    // bz_gemv then reports)
+    // a malformed descriptor is refused before the first call on a device
+    // sets up (and clears) its scratch
+    const int rc0 = bz::gemv_check_desc(d);
+    if (rc0 != BZ_OK) return rc0;
     if (bz_gemv_workspace(d) > BZ_GEMV_SCRATCH_BYTES) return BZ_ERR_SCRATCH;
     uint8_t* ws = nullptr;
     const int rc = bz::device_scratch(static_cast<hipStream_t>(stream), &ws);

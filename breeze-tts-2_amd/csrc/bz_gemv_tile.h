@@ -478,4 +478,8 @@ int launch_tile_bf16(const TileParams& tp, const TileLaunch& l, hipStream_t st);
 int launch_tile_i4t(const TileParams& tp, const TileLaunch& l, hipStream_t st);
 int launch_tile_f8t(const TileParams& tp, const TileLaunch& l, hipStream_t st);
 
+// The descriptor checks of bz_gemv (bz_gemv.hip), without launching: BZ_OK or
+// the status bz_gemv would return for a malformed descriptor.
+int gemv_check_desc(const bz_gemv_desc* d);
+
 }  // namespace bz

@@ -10,9 +10,12 @@
  *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
  *   - No call allocates memory, synchronizes the host or tunes anything, so
  *     every call can be recorded into a HIP graph.  Calls on different
- *     streams are independent: no call keeps global mutable device state.
+ *     streams are independent as long as they do not share a workspace (the
+ *     caller's; bz_gemv_noalloc is the one exception: its static array is one
+ *     per GPU, shared by every stream, see there).
  *   - Return value: BZ_OK (0) or a bz_status error code; bz_strerror() names
- *     it.  Errors are detected on the host before anything is launched.
+ *     it.  Invalid descriptors and arguments are rejected on the host before
+ *     anything is launched.
  *   - bfloat16 tensors are raw uint16 bit patterns; "bf16" below.
  */
 #ifndef BZ_GEMV_H
@@ -73,9 +76,10 @@ typedef enum bz_status {
  *   8b .. 8b+7 then up rows 8b .. 8b+7 (logical rows 8b+r and N/2+8b+r), so a
  *   block finishes 8 outputs silu(g) * u.  Only valid with BZ_EPI_SILU_GATE;
  *   the unpaired tiled formats do not take that epilogue.
- * The tiled formats run on GEMV path 5 only (M <= 8 rows per launch; more
- * rows run as several launches) and need K % 128 == 0 (int4) or
- * K % 64 == 0 (fp8); int4 group must be 128.
+ * The tiled formats run on GEMV path 5, the streaming kernel (M <= 8 rows
+ * per launch; more rows run as several launches), and the unpaired ones also
+ * on the several-row paths 4 and 6 (see below).  They need K % 128 == 0
+ * (int4) or K % 64 == 0 (fp8); int4 group must be 128.
  */
 typedef enum bz_wfmt {
     BZ_W_INT4_ZP = 0,
@@ -182,6 +186,15 @@ int bz_abi_version(void);
 
 /* Static description of a status code. */
 const char* bz_strerror(int status);
+
+/* Host helper, no counterpart in the reference: *active = 1 and *id = the
+ * capture's id while a graph capture is under way on `stream`, else 0 and 0.
+ * Launches nothing.  The torch binding keys its GEMV and attention
+ * workspaces by (device, stream) and, during a capture, by the capture, so
+ * calls on different streams and different captured graphs never share one
+ * (the reference's one cached partial buffer per device,
+ * models/fused/kernels.py:179,192-198, is shared by every stream). */
+int bz_stream_capture(void* stream, int32_t* active, uint64_t* id);
 
 /* Workspace bytes the several-row tile path (path 4) needs for this
  * descriptor: 0 when bz_gemv would not take that path (M < 5 without

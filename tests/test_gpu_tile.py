@@ -239,15 +239,17 @@ def test_tile_every_instance_steady_loop(fmt, depth, tiles, M, waves):
     _check(call(x, cfg=(depth, waves, tiles, PATH, 1), out_dtype=torch.float32), x, w_eff, rs=rs)
 
 
+def _ws_key(stream: torch.cuda.Stream, capture=None):
+    return (torch.cuda.current_device(), stream.cuda_stream, capture)
+
+
 def test_tile_graph_survives_workspace_growth():
-    """A graph captured over the device's GEMV workspace keeps working after
-    a larger call has grown (replaced) that workspace: the outgrown buffer
-    stays alive."""
+    """A graph captured over a tile-path GEMV gets a workspace of its own
+    (allocated from the graph's pool, its zero fill recorded in the graph),
+    and keeps working after an eager call on the capture stream has grown
+    (replaced) that stream's workspace: the outgrown buffer stays alive."""
     from breeze_amd import gemv as gemv_mod
 
-    dev = torch.cuda.current_device()
-    if dev in gemv_mod._GEMV_WS:  # start from a fresh (small) workspace, whatever ran before
-        gemv_mod._GEMV_WS_RETIRED.append(gemv_mod._GEMV_WS.pop(dev))
     c = Int4Case(O.synth(200, 1280, 1, seed=26)[0], 128)
     x = bf16_tensor(O.synth(8, 1280, 16, seed=27)[2])
     out = torch.empty(16, 200, device="cuda", dtype=torch.bfloat16)
@@ -255,30 +257,76 @@ def test_tile_graph_survives_workspace_growth():
     def run():
         G.gemv(x, c.d_packed, G.W_INT4_ZP, 200, sc0=c.d_sz, group=128, out=out, cfg=(0, 0, 0, PATH, 5))
 
-    run()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        gemv_mod._GEMV_WS.pop(_ws_key(s), None)  # start from a fresh (small) workspace on s
+        run()
+    torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     eager = out.clone()
+    before = gemv_mod._GEMV_WS[_ws_key(s)]
+    n_graph = sum(1 for k in gemv_mod._GEMV_WS if k[2] is not None)
     g = torch.cuda.CUDAGraph()
-    s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s), torch.cuda.graph(g, stream=s):
         run()
     torch.cuda.current_stream().wait_stream(s)
-    before = gemv_mod._GEMV_WS[dev]
-    # a split-K call needing more than the fresh 1 MiB workspace grows it
+    graph_bufs = [v for k, v in gemv_mod._GEMV_WS.items() if k[2] is not None]
+    assert len(graph_bufs) == n_graph + 1  # the capture's own workspace
+    assert all(b.data_ptr() != before.data_ptr() for b in graph_bufs)
+    # a split-K call on s needing more than the fresh 1 MiB workspace grows s's
     big = Int4Case(O.synth(2048, 2560, 1, seed=28)[0], 128)
     xb_bits = O.synth(8, 2560, 32, seed=29)[2]
     assert 20 * 32 * 2048 * 4 > before.numel() * 4
-    got = G.gemv(bf16_tensor(xb_bits), big.d_packed, G.W_INT4_ZP, 2048, sc0=big.d_sz, group=128,
-                 cfg=(0, 0, 0, PATH, 20))
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        got = G.gemv(bf16_tensor(xb_bits), big.d_packed, G.W_INT4_ZP, 2048, sc0=big.d_sz, group=128,
+                     cfg=(0, 0, 0, PATH, 20))
+    torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-    assert gemv_mod._GEMV_WS[dev].data_ptr() != before.data_ptr()
+    assert gemv_mod._GEMV_WS[_ws_key(s)].data_ptr() != before.data_ptr()
     _check(got, xb_bits, big.w_zp)
     for i in range(3):
         out.zero_()
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), i
+        run()  # eager work on the current stream between the replays
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+
+
+def test_tile_two_streams_own_workspaces():
+    """Split-K tile GEMVs issued on two streams at once: each stream uses a
+    workspace of its own (different buffers), and both results equal the
+    ones the same calls give one after the other on one stream."""
+    from breeze_amd import gemv as gemv_mod
+
+    N, K, M = 2560, 10240, 32
+    cases = [Int4Case(O.synth(N, K, 1, seed=40 + i)[0], 128) for i in range(2)]
+    xs = [bf16_tensor(O.synth(8, K, M, seed=42 + i)[2]) for i in range(2)]
+
+    def call(i):
+        return G.gemv(xs[i], cases[i].d_packed, G.W_INT4_ZP, N, sc0=cases[i].d_sz, group=128,
+                      cfg=(0, 0, 0, PATH, 10))
+
+    serial = [call(0), call(1)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(2)]
+    outs = [None, None]
+    for rep in range(4):
+        for i, st in enumerate(streams):
+            st.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(st):
+                outs[i] = call(i)
+        for st in streams:
+            torch.cuda.current_stream().wait_stream(st)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], serial[0]) and torch.equal(outs[1], serial[1]), rep
+    bufs = [gemv_mod._GEMV_WS[_ws_key(st)] for st in streams]
+    assert bufs[0].data_ptr() != bufs[1].data_ptr()
+    _check(outs[0], O.f32_to_bf16_bits(xs[0].float().cpu().numpy()), cases[0].w_zp)
 
 
 @pytest.mark.parametrize("fmt", ["int4", "fp8"])

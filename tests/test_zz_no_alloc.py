@@ -144,3 +144,115 @@ def test_noalloc_refuses_oversized_workspace_without_launching():
     assert lib.bz_gemv_noalloc(ctypes.byref(d), L.stream_of(x)) == L.ERR_SCRATCH
     torch.cuda.synchronize()
     assert torch.count_nonzero(out) == 0
+
+
+def _capture_noalloc(calls):
+    """Record bz_gemv_noalloc calls [(desc, x)] into one graph on a side stream."""
+    lib = L.lib()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(st), torch.cuda.graph(g, stream=st):
+        for d, _ in calls:
+            L.check(lib.bz_gemv_noalloc(ctypes.byref(d), st.cuda_stream), "bz_gemv_noalloc")
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    return g
+
+
+def test_noalloc_under_graph_capture():
+    """Tile-path calls (down K10240 N2560 at M = 16, then M = 6, split-K
+    partials in the scratch) recorded into a HIP graph and replayed three
+    times, with eager bz_gemv_noalloc and torch work between the replays:
+    every replay gives bz_gemv's result bit for bit."""
+    N, K = 2560, 10240
+    w, sc, _ = _int4(N, K, 11)
+    calls, refs, outs = [], [], []
+    for m in (16, 6):
+        x = _x(m, K, 40 + m)
+        ref, _, need = _both(x, w, G.W_INT4_ZP, N, sc0=sc)
+        assert need > 0
+        out = torch.zeros(m, N, device="cuda", dtype=torch.bfloat16)
+        calls.append((_desc(x, w, G.W_INT4_ZP, N, sc0=sc, out=out), x))
+        refs.append(ref)
+        outs.append(out)
+    g = _capture_noalloc(calls)
+    lib = L.lib()
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for o, r in zip(outs, refs):
+            assert torch.equal(o, r), rep
+        # eager use of the same scratch between replays (a shorter call)
+        x = _x(5, K, 70 + rep)
+        ref, got, _ = _both(x, w, G.W_INT4_ZP, N, sc0=sc)
+        assert torch.equal(got, ref), rep
+        torch.randn(1 << 20, device="cuda").sum().item()
+    del g, lib
+
+
+_FIRST_CALL_CHILD = r"""
+import ctypes, sys
+sys.path[:0] = [{root!r}, {pkg!r}]
+import torch
+from breeze_amd import _lib as L
+from breeze_amd import gemv as G
+torch.manual_seed(0)
+N, K, M = 2560, 10240, 16
+w = torch.randn(N, K, device="cuda") * 0.02
+packed, sz, _ = G.quantize_int4_device(w, 128, True, G.W_INT4_ZP)
+x = torch.randn(M, K, device="cuda").to(torch.bfloat16)
+torch.cuda.synchronize()
+
+def desc(out):
+    d = L.GemvDesc()
+    d.abi_version = L.ABI_VERSION
+    d.M, d.N, d.K, d.group, d.wfmt = M, N, K, 128, G.W_INT4_ZP
+    d.out_dtype = d.residual_dtype = L.DT_BF16
+    d.eps = 1e-6
+    d.x, d.ldx, d.w, d.sc0 = x.data_ptr(), x.stride(0), packed.data_ptr(), sz.data_ptr()
+    d.out, d.ldo = out.data_ptr(), out.stride(0)
+    return d
+
+lib = L.lib()
+got = torch.zeros(M, N, device="cuda", dtype=torch.bfloat16)
+st = torch.cuda.Stream()
+st.wait_stream(torch.cuda.current_stream())
+g = torch.cuda.CUDAGraph()
+d = desc(got)
+assert lib.bz_gemv_workspace(ctypes.byref(d)) > 0
+with torch.cuda.stream(st), torch.cuda.graph(g, stream=st):
+    # the process's first bz_gemv_noalloc call on this device, under capture
+    rc = lib.bz_gemv_noalloc(ctypes.byref(d), st.cuda_stream)
+torch.cuda.current_stream().wait_stream(st)
+assert rc == 0, rc
+ref = torch.empty_like(got)
+dr = desc(ref)
+ws = torch.zeros(lib.bz_gemv_workspace(ctypes.byref(dr)) // 4 + 4, dtype=torch.int32, device="cuda")
+dr.workspace, dr.workspace_bytes = ws.data_ptr(), ws.numel() * 4
+assert lib.bz_gemv(ctypes.byref(dr), L.stream_of(x)) == 0
+for rep in range(3):
+    got.fill_(float("nan"))
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref), rep
+print("FIRST_CALL_UNDER_CAPTURE_OK", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture_in_fresh_process():
+    """In a fresh child process, the first bz_gemv_noalloc call (which looks
+    up the device's scratch address and records its counter clear) is made
+    under graph capture; the replays equal bz_gemv's result bit for bit."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    code = _FIRST_CALL_CHILD.format(root=str(root), pkg=str(root / "breeze-tts-2_amd"))
+    print("child: first bz_gemv_noalloc call under capture, K10240 N2560 M16", flush=True)
+    res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=110)
+    assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-3000:]
+    assert "FIRST_CALL_UNDER_CAPTURE_OK" in res.stdout
