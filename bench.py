@@ -174,11 +174,19 @@ def main() -> int:
                     help="only build and time the depth-decoder frame graph, for kernel-trace runs")
     ap.add_argument("--mfma-summary", nargs=2, metavar=("TRACE_DIR", "PMC_DIR"),
                     help="summarize a rocprofv3 --kernel-trace run and a --pmc run of --profile-tiles")
+    ap.add_argument("--profile-step", type=int, metavar="M",
+                    help="only build the 26-layer decode step at M rows (tiled layout) and replay its graph, "
+                         "for kernel-trace runs")
+    ap.add_argument("--step-summary", metavar="TRACE_DIR",
+                    help="per-kernel breakdown of the decode-step replays in a rocprofv3 --kernel-trace run of "
+                         "--profile-step")
     args = ap.parse_args()
     if args.pmc_summary:
         return pmc_summary(*args.pmc_summary)
     if args.mfma_summary:
         return mfma_summary(*args.mfma_summary)
+    if args.step_summary:
+        return step_summary(args.step_summary)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the decode GEMVs here run "
               "on a single MI355X and no multi-GPU path is built).", file=sys.stderr)
@@ -203,6 +211,10 @@ def main() -> int:
         return profile_tiles(torch, G, dev)
     if args.profile_gemvs:
         return profile_gemvs(torch, G, dev)
+    if args.profile_step:
+        print(json.dumps({"decode_step": decode_step(torch, G, dev, log, args.profile_step, reps=STEP_REPS)}),
+              flush=True)
+        return 0
     if args.profile_depth:
         print(json.dumps({"depth_frame": depth_frame(torch, dev, log)}), flush=True)
         return 0
@@ -356,6 +368,7 @@ def main() -> int:
         detail["depth_frame"] = depth_frame(torch, dev, log)
     if not args.no_configs:
         detail["configs"] = config_table(torch, G, dev, log)
+        detail["modules"] = module_table(torch, dev, log)
         detail["library_bf16_linear"] = library_table(torch, dev, log)
         detail["attention"] = attention_table(torch, dev, log)
         detail["fp32_heads"] = heads_table(torch, dev, log)
@@ -459,6 +472,9 @@ def compact(out: dict) -> dict:
             gemvs[f"{r['config'].split(' ')[0]} {r['config'].split(' ', 1)[1]} M{r['M']}"] = [r["us"], r["frac"]]
     if gemvs:
         s["gemv_us_frac"] = gemvs
+    mods = {f"{r['module']} M{r['M']}": [r["us"], r["frac"]] for r in d.get("modules", [])}
+    if mods:
+        s["module_us_frac"] = mods
     head["summary"] = s
     if len(json.dumps(head)) > SUMMARY_MAX_CHARS:  # never: trimmed from the largest optional part first
         s.pop("gemv_us_frac", None)
@@ -853,6 +869,63 @@ def config_table(torch, G, dev, log) -> list:
     return rows
 
 
+# (module class, name, N, K): the reference-named Linear modules at the
+# decode shapes, called as a model calls them (forward on [M, K] bf16).
+MODULE_SHAPES = [
+    ("Int4Linear", "down K10240 N2560", 2560, 10240),
+    ("Fp8Linear", "down K10240 N2560", 2560, 10240),
+    ("Fp8Linear", "gate K2560 N10240", 10240, 2560),
+]
+
+
+def module_table(torch, dev, log) -> list:
+    """Int4Linear / Fp8Linear forward (models/int4_linear.py:99-109,
+    models/fp8_linear.py:68-84) at M = 1 and 2 on N(0, 0.02) weights (int4
+    with the reference's asymmetric quantizer, group 128), timed as HIP-graph
+    replays over module copies whose buffers span >= 1 GiB.  Roofline bytes:
+    the buffers the forward reads (the tiled weight with its scales) + x +
+    output."""
+    import copy
+
+    from breeze_amd.fp8_linear import Fp8Linear
+    from breeze_amd.fused.kernels import graph_time_us
+    from breeze_amd.int4_linear import Int4Linear
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    rows = []
+    for cls_name, name, N, K in MODULE_SHAPES:
+        lin = torch.nn.Linear(K, N, bias=False, device=dev)
+        with torch.no_grad():
+            lin.weight.copy_(torch.randn(N, K, device=dev, generator=gen) * 0.02)
+        mod = Int4Linear(lin) if cls_name == "Int4Linear" else Fp8Linear(lin)
+        del lin
+        buf = mod.weight_int4 if cls_name == "Int4Linear" else mod.weight_fp8
+        wbytes = buf.numel() * buf.element_size()
+        mods = [copy.deepcopy(mod) for _ in range(max(2, -(-(1 << 30) // wbytes)))]
+        for M in (1, 2):
+            x = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
+            st = {"i": 0}
+
+            def call():
+                mods[st["i"] % len(mods)](x)
+                st["i"] += 1
+
+            if M == 1:
+                graph_time_us(call, iters=min(2 * len(mods), 64))
+            us = graph_time_us(call, iters=2 * len(mods))
+            nbytes = wbytes + 2 * M * K + 2 * M * N
+            roof = nbytes / HBM_PEAK_GBPS / 1e3
+            rows.append({"module": f"{cls_name} {name}", "M": M, "us": round(us, 2),
+                         "gbps": round(nbytes / us / 1e3, 1), "roofline_us": round(roof, 2),
+                         "frac": round(roof / us, 3)})
+            log(f"{cls_name} {name} M={M}: {us:6.2f} us ({nbytes / us / 1e3:5.0f} GB/s, "
+                f"{roof / us * 100:4.1f}% of roofline)")
+        del mods, mod
+        torch.cuda.empty_cache()
+    return rows
+
+
 def attention_table(torch, dev, log) -> list:
     """The fused decode-attention step alone (q/k RMSNorm + RoPE + cache
     write + attention over cache positions [0, pos] + split combine) of the
@@ -950,8 +1023,64 @@ def heads_table(torch, dev, log) -> list:
     return rows
 
 
+# Timed replays of the decode-step graph (the last STEP_REPS x STEP_KERNELS
+# GEMV dispatches of a --profile-step run); 26 layers x 4 GEMVs + the head.
+STEP_REPS = 20
+STEP_KERNELS = 26 * 4 + 1
+
+
+def step_summary(trace_dir: str) -> int:
+    """Where a decode step's time goes, from a rocprofv3 --kernel-trace run
+    of --profile-step: the last STEP_REPS replays of the graph (STEP_KERNELS
+    GEMV launches each), per kernel the calls per step, the average and the
+    sum of their durations, then the gaps between the end of one launch and
+    the start of the next and the step's span from the first start to the
+    last end (medians over the replays)."""
+    import csv
+    import glob
+    import statistics
+
+    paths = glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True)
+    if not paths:
+        raise SystemExit(f"no kernel_trace.csv under {trace_dir}")
+    rows = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"])
+                  for r in csv.DictReader(open(paths[0])) if "gemv_" in r["Kernel_Name"])
+    need = STEP_REPS * STEP_KERNELS
+    if len(rows) < need:
+        raise SystemExit(f"{len(rows)} GEMV dispatches, fewer than {need}")
+    steps = [rows[len(rows) - need + i * STEP_KERNELS:len(rows) - need + (i + 1) * STEP_KERNELS]
+             for i in range(STEP_REPS)]
+
+    def short(name):
+        m = re.search(r"(gemv_\w+<[^>]*>)", name)
+        return m.group(1) if m else name[:60]
+
+    per = {}
+    for st in steps:
+        seen = {}
+        for t0, t1, name in st:
+            seen.setdefault(short(name), []).append((t1 - t0) / 1e3)
+        for k, v in seen.items():
+            per.setdefault(k, []).append(v)
+    spans = [(st[-1][1] - st[0][0]) / 1e3 for st in steps]
+    busy = [sum(t1 - t0 for t0, t1, _ in st) / 1e3 for st in steps]
+    gaps = [[(st[i + 1][0] - st[i][1]) / 1e3 for i in range(len(st) - 1)] for st in steps]
+    print(f"decode step: {STEP_KERNELS} GEMV launches per step, median over {STEP_REPS} graph replays")
+    print(f"{'kernel':40s} {'calls':>5s} {'avg us':>8s} {'sum us':>8s}")
+    for k, v in sorted(per.items(), key=lambda kv: -statistics.median(sum(x) for x in kv[1])):
+        calls = len(v[0])
+        print(f"{k:40s} {calls:5d} {statistics.median(statistics.mean(x) for x in v):8.2f} "
+              f"{statistics.median(sum(x) for x in v):8.1f}")
+    flat = sorted(g for gs in gaps for g in gs)
+    print(f"kernel time per step {statistics.median(busy):.1f} us; gaps between launches: median "
+          f"{statistics.median(flat):.2f} us, 90th percentile {flat[int(0.9 * len(flat))]:.2f} us, "
+          f"sum per step {statistics.median(sum(g) for g in gaps):.1f} us; span first start to last end "
+          f"{statistics.median(spans):.1f} us")
+    return 0
+
+
 def decode_step(torch, G, dev, log, M: int = 1, attn_pos: int | None = None, cache_len: int = 1024,
-                layout: str = "tiled") -> dict:
+                layout: str = "tiled", reps: int = 20) -> dict:
     """26 decoder layers (hidden 2560, 16x256 q heads, 4 KV heads, MLP 10240)
     of int4 group-128 weights: RMSNorm->QKV, attention replaced by a copy of
     the [M, 4096] query part, o_proj + residual, RMSNorm->gate|up SiLU-gate,
@@ -1055,7 +1184,6 @@ def decode_step(torch, G, dev, log, M: int = 1, attn_pos: int | None = None, cac
         g.replay()
     torch.cuda.synchronize()
     replay_checksum = float(logits.double().sum().item())
-    reps = 20
     s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s_ev.record()
     for _ in range(reps):

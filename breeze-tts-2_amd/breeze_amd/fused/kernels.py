@@ -157,12 +157,22 @@ class FusedWeight:
     @classmethod
     def from_fp8(cls, *mods, paired: bool = False) -> "FusedWeight":
         """Adopt Fp8Linear buffers, stacked along N (models/fused/layer.py:
-        20-29): tiled when the shape allows, else concatenated as they are."""
+        20-29): tiled modules re-tiled into one weight (paired for gate|up),
+        row-major ones tiled when the stacked shape allows, else
+        concatenated as they are."""
+        from ..fp8_linear import LAYOUT_TILED as FP8_TILED
+        from ..fp8_linear import layout_of as fp8_layout_of
         N, K = _stack_shape(mods, paired)
         if K % 16:
             raise ValueError(f"fp8 weights with in_features {K} (not a multiple of 16) cannot be fused")
-        parts = [(W_FP8, m.weight_fp8.view(torch.uint8), m.weight_scale.reshape(-1).float(), m.out_features)
-                 for m in mods]
+        layouts = {fp8_layout_of(m.weight_fp8, m.out_features, m.in_features) for m in mods}
+        if layouts == {FP8_TILED}:
+            parts = [(W_FP8_TILED, m.weight_fp8.view(torch.uint8), None, m.out_features) for m in mods]
+        elif FP8_TILED in layouts:
+            raise ValueError("fp8 modules in different layouts cannot be fused")
+        else:
+            parts = [(W_FP8, m.weight_fp8.view(torch.uint8), m.weight_scale.reshape(-1).float(), m.out_features)
+                     for m in mods]
         tiled = _tile_rows(8, paired, parts, N, K)
         if tiled is not None:
             return cls._assemble(8, GROUP, N, K, "tiled-paired" if paired else "tiled", tiled)

@@ -47,6 +47,7 @@ __all__ = [
     "quantize_int4_device",
     "quantize_fp8_device",
     "dequant",
+    "dequant_matmul",
     "EPI_NONE",
     "EPI_SILU_GATE",
     "EPI_RESIDUAL",
@@ -482,4 +483,31 @@ def dequant(wfmt: int, w: torch.Tensor, n: int, k: int, *, sc0=None, sc1=None, g
                               _lib.stream_of(w)),
         "bz_dequant",
     )
+    return out
+
+
+def dequant_matmul(x: torch.Tensor, w: torch.Tensor, wfmt: int, n: int, k: int,
+                   chunk_bytes: int = 16 << 20) -> torch.Tensor:
+    """x [M, k] @ w_eff^T -> bf16 [M, n] for prefill-sized M, over an unpaired
+    tiled weight (BZ_W_INT4_TILED, group 128, or BZ_W_FP8_TILED).  The weight
+    is decoded by the GPU path's own unpacking (bz_dequant) one run of whole
+    16-row blocks at a time, at most ``chunk_bytes`` of fp32 per run, each
+    run cast to bf16 and multiplied by torch's GEMM into its output columns:
+    the transient memory stays bounded whatever the weight's size (a whole
+    fp32 copy of a 10240 x 2560 weight would be 105 MB)."""
+    if wfmt not in (W_INT4_TILED, W_FP8_TILED):
+        raise ValueError(f"dequant_matmul reads the unpaired tiled formats, not format {wfmt}")
+    _require_gpu("x", x, x.device)
+    _check_weight(w, wfmt, n, k, 128, None, None)
+    if x.dim() != 2 or x.shape[1] != k:
+        raise ValueError(f"x must be [M, {k}], got {tuple(x.shape)}")
+    x = x.to(torch.bfloat16)
+    block = tiled_bytes(wfmt, 16, k)
+    wb = w.contiguous().view(torch.uint8).reshape(-1)
+    rows = max(16, chunk_bytes // (4 * k) // 16 * 16)
+    out = torch.empty(x.shape[0], n, device=x.device, dtype=torch.bfloat16)
+    for r0 in range(0, n, rows):
+        r = min(rows, n - r0)
+        part = wb[(r0 // 16) * block:((r0 + r) // 16) * block]
+        out[:, r0:r0 + r] = torch.nn.functional.linear(x, dequant(wfmt, part, r, k).to(torch.bfloat16))
     return out

@@ -38,7 +38,8 @@ import torch
 from torch import nn
 
 from ._swap import swap_linears
-from .gemv import W_INT4_TILED, W_INT4_ZP, dequant, gemv_traceable, pack_tiled, quantize_int4_device, tiled_bytes
+from .gemv import (W_INT4_TILED, W_INT4_ZP, dequant_matmul, gemv_traceable, pack_tiled, quantize_int4_device,
+                   tiled_bytes)
 
 GROUP_SIZE = 128
 
@@ -49,8 +50,8 @@ MIN_QUANT_BYTES = 8 * 1024 * 1024
 DEFAULT_TARGET_NAMES = ("gate_proj", "up_proj", "down_proj")
 
 # Above this many rows a call is a prefill rather than a decode step: a tiled
-# weight is then decoded once to bf16 and multiplied by the library GEMM,
-# instead of being streamed once per slice of 8 rows by the decode kernel.
+# weight is then decoded to bf16 in bounded row chunks and multiplied by the
+# library GEMM, instead of being streamed once per 32 rows by the GEMV.
 PREFILL_ROWS = 32
 
 # Tags recorded by the checkpoint manifest for the two packed layouts.
@@ -149,8 +150,7 @@ class Int4Linear(nn.Module):
         if layout_of(self.weight_int4, self.out_features, self.in_features) == LAYOUT_TILED:
             wfmt, sc0 = W_INT4_TILED, None
             if flat.shape[0] > PREFILL_ROWS and not torch.compiler.is_compiling():
-                w = dequant(W_INT4_TILED, self.weight_int4, self.out_features, self.in_features)
-                out = flat.to(torch.bfloat16) @ w.to(torch.bfloat16).t()
+                out = dequant_matmul(flat, self.weight_int4, W_INT4_TILED, self.out_features, self.in_features)
                 return out.to(x.dtype).reshape(*shape[:-1], self.out_features)
         else:
             wfmt, sc0 = W_INT4_ZP, self.scales_zeros

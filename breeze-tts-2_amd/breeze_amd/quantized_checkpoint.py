@@ -21,7 +21,12 @@ This build's additions to the manifest and the loader:
 * the buffer shapes of every entry are checked against its features and
   group before any buffer is made, so a manifest that does not describe a
   buffer the GEMV can read fails at load time, not on the GPU;
-* Fp8Linear modules are recorded too (kind "fp8");
+* Fp8Linear modules are recorded too (kind "fp8"), with ``"layout"`` the
+  tag of their weight_fp8 bytes (fp8_linear.LAYOUT_TILED,
+  "bz-fp8-tiled16-v1", or LAYOUT_ROWMAJOR, "e4m3-rowmajor", the reference's
+  [N, K] codes).  An fp8 entry without a tag is the reference's row-major
+  buffer and is read as such; a row-major module of a tileable shape is
+  re-tiled on its GPU after loading;
 * ``convert_logical_int4`` turns the logical nibbles the reference's
   quantizer builds before its repack (odd k in the low nibble,
   models/int4_linear.py:57-58) into this build's row-major buffer.
@@ -42,6 +47,7 @@ from safetensors import safe_open
 from safetensors.torch import save_file
 from torch import nn
 
+from . import fp8_linear as _f8
 from .fp8_linear import FP8_DTYPE, Fp8Linear
 from .int4_linear import LAYOUT_ROWMAJOR, LAYOUT_TILED, Int4Linear, layout_of, retile, tileable, tiled_shape
 
@@ -101,7 +107,17 @@ def _int4_shapes(spec: dict) -> dict:
 
 def _fp8_shapes(spec: dict) -> dict:
     n, k = spec["out_features"], spec["in_features"]
-    return {"weight_fp8": [n, k], "weight_scale": [1, n]}
+    layout = spec.get("layout", _f8.LAYOUT_ROWMAJOR)  # untagged: the reference's own [N, K] codes
+    if layout == _f8.LAYOUT_TILED:
+        if not _f8.tileable(n, k):
+            raise ValueError(f"a {n}x{k} fp8 weight has no tiled layout")
+        codes = list(_f8.tiled_shape(n, k))
+    elif layout == _f8.LAYOUT_ROWMAJOR:
+        codes = [n, k]
+    else:
+        raise ValueError(f"fp8 module stored in layout {layout!r}; this build reads {_f8.LAYOUT_TILED!r} and "
+                         f"{_f8.LAYOUT_ROWMAJOR!r}")
+    return {"weight_fp8": codes, "weight_scale": [1, n]}
 
 
 _KINDS = (
@@ -127,6 +143,8 @@ def describe(model: nn.Module) -> dict[str, dict]:
         entry = {"kind": kind.name}
         if kind.name == "int4":
             entry["layout"] = layout_of(module.weight_int4, module.out_features, module.in_features)
+        elif kind.name == "fp8":
+            entry["layout"] = _f8.layout_of(module.weight_fp8, module.out_features, module.in_features)
         entry.update({a: int(getattr(module, a)) for a in kind.attrs})
         entry["shapes"] = {b: list(getattr(module, b).shape) for b in kind.buffers}
         entries[path] = entry
@@ -190,8 +208,8 @@ def install_shells(model: nn.Module, manifest: dict, device) -> int:
 def load_quantized_state(model: nn.Module, out_dir: Path, device, host_prefixes: tuple[str, ...] = ()) -> dict:
     """Load the checkpoint into ``model`` (shells installed), tensors on
     ``device`` except those whose name starts with one of ``host_prefixes``,
-    which stay in host memory.  Row-major int4 modules of a tileable shape are
-    re-tiled when they land on a GPU.  Returns counts and a few names of
+    which stay in host memory.  Row-major int4 and fp8 modules of a tileable
+    shape are re-tiled when they land on a GPU.  Returns counts and a few names of
     missing and unexpected keys."""
     state = {}
     with safe_open(str(Path(out_dir) / WEIGHTS_NAME), framework="pt", device="cpu") as reader:
@@ -202,6 +220,8 @@ def load_quantized_state(model: nn.Module, out_dir: Path, device, host_prefixes:
     for module in model.modules():
         if isinstance(module, Int4Linear) and module.weight_int4.is_cuda:
             retile(module)
+        elif isinstance(module, Fp8Linear) and module.weight_fp8.is_cuda:
+            _f8.retile(module)
     missing, unexpected = list(result.missing_keys), list(result.unexpected_keys)
     return {
         "loaded": len(state),

@@ -253,9 +253,10 @@ def dequant_int4_zp(q, sz_bits, group: int = GROUP) -> np.ndarray:
     q = np.asarray(q, dtype=np.uint8)
     n, k = q.shape
     sz = bf16_bits_to_f32(sz_bits)  # [G, N, 2]
-    s = np.repeat(sz[..., 0].T, group, axis=1)
-    z = np.repeat(sz[..., 1].T, group, axis=1)
-    return ((q.astype(np.float32) - np.float32(8.0)) * s + z).astype(np.float32)
+    s = np.ascontiguousarray(sz[..., 0].T)[:, :, None]  # [N, G, 1], broadcast over the group's k
+    z = np.ascontiguousarray(sz[..., 1].T)[:, :, None]
+    qg = q.reshape(n, k // group, group).astype(np.float32)
+    return ((qg - np.float32(8.0)) * s + z).reshape(n, k).astype(np.float32, copy=False)
 
 
 def dequant_int4_min(q, s_bits, m_bits, group: int = GROUP) -> np.ndarray:

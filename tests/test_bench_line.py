@@ -41,6 +41,8 @@ def _full_record(b) -> dict:
         "depth_frame": {"us": 4917.6, "algorithmic_bytes": 5543600000, "roofline_us": 692.95, "x_roofline": 7.1,
                         "positions": 16, "layers": 12, "batch": 2, "weights": "fp8"},
         "configs": configs,
+        "modules": [{"module": f"{c} {n}", "M": m, "us": 7.41, "gbps": 3554.0, "roofline_us": 3.28, "frac": 0.443}
+                    for c, n, _, _ in b.MODULE_SHAPES for m in (1, 2)],
         "library_bf16_linear": [{"shape": "gate|up K2560 N20480", "M": 1, "us": 47.3}] * 8,
         "attention": [{"what": "z" * 80}] * 12, "fp32_heads": [{"head": "h" * 60}] * 6,
     }
@@ -75,6 +77,7 @@ def test_summary_line_is_short_and_complete():
     assert steps["c5_m1"]["us"] == 565.19 and steps["c5_m2"]["x_roofline"] == 3.028
     # the C1-C3 tiled decode GEMVs at M = 1 and 2: 14 rows
     assert len(got["summary"]["gemv_us_frac"]) == 14
+    assert len(got["summary"]["module_us_frac"]) == 2 * len(b.MODULE_SHAPES)
 
 
 def test_summary_without_optional_parts():
@@ -85,3 +88,29 @@ def test_summary_without_optional_parts():
     got = json.loads(json.dumps(b.compact(full)))
     assert got["cpu_baseline"] is None
     assert got["summary"] == {"gate_up_us": 7.0, "down_us": 5.0}
+
+
+def test_step_summary_reads_a_kernel_trace(tmp_path, capsys):
+    """--step-summary over a synthetic kernel trace: the last STEP_REPS x
+    STEP_KERNELS GEMV dispatches are the timed replays; per-kernel calls and
+    sums, gaps and span come out of their timestamps."""
+    b = _bench()
+    lines = ["Kernel_Name,Start_Timestamp,End_Timestamp"]
+    t = 0
+    lines.append(f'"void bz::quantize_int4_kernel(int)",{t},{t + 500}')   # not a GEMV: ignored
+    t += 1000
+    for rep in range(b.STEP_REPS + 2):       # two untimed replays first
+        for i in range(b.STEP_KERNELS):
+            name = "void bz::gemv_stream<5, 1, 4>(bz::StreamParams)" if i % 4 == 2 else \
+                "void bz::gemv_stream<4, 1, 5>(bz::StreamParams)"
+            lines.append(f'"{name}",{t},{t + 4000}')
+            t += 4000 + 1500                 # 4 us kernels, 1.5 us gaps
+    d = tmp_path / "trace" / "host"
+    d.mkdir(parents=True)
+    (d / "run_kernel_trace.csv").write_text("\n".join(lines) + "\n")
+    assert b.step_summary(str(tmp_path / "trace")) == 0
+    out = capsys.readouterr().out
+    assert "gemv_stream<5, 1, 4>" in out and "gemv_stream<4, 1, 5>" in out
+    assert "gaps between launches: median 1.50 us" in out
+    span = b.STEP_KERNELS * 4.0 + (b.STEP_KERNELS - 1) * 1.5
+    assert f"span first start to last end {span:.1f} us" in out

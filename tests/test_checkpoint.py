@@ -15,7 +15,9 @@ from torch import nn
 from oracle import bz_oracle as O
 
 from breeze_amd import quantized_checkpoint as Q
+from breeze_amd import fp8_linear as F8
 from breeze_amd.fp8_linear import Fp8Linear
+from breeze_amd.fp8_linear import tiled_shape as fp8_tiled_shape
 from breeze_amd.int4_linear import LAYOUT_ROWMAJOR, LAYOUT_TILED, Int4Linear, tiled_shape
 
 
@@ -30,11 +32,14 @@ def _int4_shell(n, k, g, gen, tiled=False):
     return m
 
 
-def _fp8_shell(n, k, gen):
+def _fp8_shell(n, k, gen, tiled=False):
+    """An Fp8Linear holding random codes: tiled [N/16, 16 K + 128] or the
+    reference's row-major [N, K]."""
     m = Fp8Linear.__new__(Fp8Linear)
     nn.Module.__init__(m)
     m.in_features, m.out_features = k, n
-    m.register_buffer("weight_fp8", torch.randn(n, k, generator=gen).to(torch.float8_e4m3fn))
+    shape = fp8_tiled_shape(n, k) if tiled else (n, k)
+    m.register_buffer("weight_fp8", torch.randn(*shape, generator=gen).to(torch.float8_e4m3fn))
     m.register_buffer("weight_scale", torch.rand(1, n, generator=gen))
     return m
 
@@ -134,6 +139,41 @@ def test_refuses_untileable_tiled_entry(tmp_path):
     man["modules"]["mlp.up_proj"]["layout"] = LAYOUT_TILED      # group 32 has no tiled layout
     with pytest.raises(ValueError, match="no tiled layout"):
         Q.install_shells(_Block(), man, "cpu")
+
+
+def test_fp8_layout_tags(tmp_path):
+    """fp8 entries carry their layout: a tiled module round-trips under
+    bz-fp8-tiled16-v1; an entry without a tag (the reference's manifest) is
+    its row-major [N, K] buffer; an unknown tag, or the tiled tag on a shape
+    that has no tiled layout, is refused."""
+    gen = torch.Generator().manual_seed(5)
+    blk = _Block()
+    blk.mlp.gate_proj = _fp8_shell(256, 128, gen, tiled=True)
+    blk.mlp.up_proj = _fp8_shell(256, 128, gen)
+    blk.mlp.down_proj = _fp8_shell(128, 256, gen, tiled=True)
+    man = Q.save_quantized(blk, tmp_path, {"fp8": "mlp"}, source="synthetic")
+    assert man["modules"]["mlp.gate_proj"]["layout"] == F8.LAYOUT_TILED
+    assert man["modules"]["mlp.gate_proj"]["shapes"]["weight_fp8"] == [16, 16 * 128 + 128]
+    assert man["modules"]["mlp.up_proj"]["layout"] == F8.LAYOUT_ROWMAJOR
+    fresh = _Block()
+    Q.install_shells(fresh, Q.read_manifest(tmp_path), "cpu")
+    assert Q.load_quantized_state(fresh, tmp_path, "cpu")["missing"] == 0
+    for name in ("gate_proj", "up_proj", "down_proj"):
+        a, b = getattr(blk.mlp, name), getattr(fresh.mlp, name)
+        assert torch.equal(a.weight_fp8.view(torch.uint8), b.weight_fp8.view(torch.uint8)), name
+    untagged = json.loads(json.dumps(man))
+    del untagged["modules"]["mlp.up_proj"]["layout"]
+    other = _Block()
+    Q.install_shells(other, untagged, "cpu")
+    assert tuple(other.mlp.up_proj.weight_fp8.shape) == (256, 128)
+    bad = json.loads(json.dumps(man))
+    bad["modules"]["mlp.up_proj"]["layout"] = "fp8-something"
+    with pytest.raises(ValueError, match="fp8 module stored in layout"):
+        Q.install_shells(_Block(), bad, "cpu")
+    bad = json.loads(json.dumps(man))
+    bad["modules"]["mlp.up_proj"].update(layout=F8.LAYOUT_TILED, in_features=100)
+    with pytest.raises(ValueError, match="no tiled layout"):
+        Q.install_shells(_Block(), bad, "cpu")
 
 
 def test_convert_logical_int4_matches_oracle_packing():

@@ -1,19 +1,37 @@
-"""The synthetic decode step of the int4 decoder at its real shape, on the GPU,
-against the oracle's dequantize-then-matmul chain.
+"""The synthetic decode step of the int4 decoder at its real shape and full
+depth, on the GPU, against the oracle.
 
-Hidden 2560, 16 query heads x 256, 4 KV heads, MLP 10240, int4 group-128
-symmetric weights; each layer is RMSNorm -> QKV GEMV (N 6144), the attention
-stand-in (the query part [M, 4096] copied), o_proj K4096 + residual,
-RMSNorm -> gate|up GEMV (N 2 x 10240) with SiLU-gate, down K10240 +
-residual; the step ends with RMSNorm -> bf16 head K2560 N8192.  Three full
-layers run here (the 26 of the timed step repeat the same launches), at
-M = 1 and M = 2, in both weight layouts: the tiled decode layout (the copy
-done by the QKV launch's second store, exactly as bench.py times it) and the
-row-major one.  The oracle rounds every intermediate to bf16 where the GPU
-path stores bf16 and computes each GEMV in float64 over W_eff; the bar on
-the logits is the stated max|out - ref| / max|ref| <= 1e-2, the comparison
-the reference makes between its fused and unfused layers
-(models/fused/test_layer.py:53-95)."""
+Hidden 2560, 16 query heads x 256, 4 KV heads, MLP 10240, 26 layers of
+int4 group-128 symmetric weights N(0, 0.02); each layer is RMSNorm -> QKV
+GEMV (N 6144), the attention stand-in (the query part [M, 4096] copied),
+o_proj K4096 + residual, RMSNorm -> gate|up GEMV (N 2 x 10240) with
+SiLU-gate, down K10240 + residual; the step ends with RMSNorm -> bf16 head
+K2560 N8192.  This is the step bench.py times, run here at M = 1 and M = 2
+in both weight layouts: the tiled decode layout (the copy done by the QKV
+launch's second store) and the row-major one.
+
+The four GPU chains and the oracle advance together one layer at a time:
+each layer's weights are drawn from the layer's own seed on the GPU,
+quantized there (the quantizer's bytes are pinned bit for bit against the
+oracle's quantizer in test_gpu_parity.py), copied to the host, decoded by
+the oracle's own unpacking and dropped before the next layer; nothing is
+cached across layers.
+
+Two checks, as the reference checks its fused layers one layer at a time on
+the same inputs (models/fused/test_layer.py:53-95):
+  * every one of the 104 GEMVs and the head, on each chain, against the
+    float64 oracle GEMV on the GPU's own inputs of that GEMV (the chain's
+    bf16 activations): <= 4e-3 against the same-rounding oracle (RMSNorm
+    folded as the kernel folds it) and <= 1e-2, the stated bar, against the
+    reference's semantics (fp32 RMSNorm, bench_gemv.py:30-53);
+  * the chain's logits against the oracle's own 26-layer chain:
+    <= CHAIN_DRIFT.  The 1e-2 bar is a per-GEMV bar: two correct
+    implementations with the same bf16 rounding points drift apart over the
+    26 layers of these weights (bf16 rounding of one intermediate flips
+    when two correct fp32 sums differ in their last bit, and the residual
+    stream carries every flip forward).  oracle/chain_drift.py measures it
+    on the CPU: float32 sums against float64 sums end 2.4e-2 apart at the
+    logits."""
 
 from __future__ import annotations
 
@@ -22,109 +40,155 @@ import pytest
 import torch
 
 from oracle import bz_oracle as O
-from tests._util import bf16_tensor, f32, u8_tensor
+from tests._util import bf16_bits, bf16_tensor, f32
 
 from breeze_amd import gemv as G
 
 pytestmark = pytest.mark.gpu
 
-H, QKV, ATT, MLP, VOCAB = 2560, 6144, 4096, 10240, 8192
-LAYERS = 3
+H, QKV, ATT, MLP, VOCAB, LAYERS = 2560, 6144, 4096, 10240, 8192, 26
+SEED = 2560
 TOL = 1e-2
-
-_STEP: dict = {}
-
-
-def _int4(n, k, rng):
-    w = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
-    q, s, z = O.quantize_int4_sym(w, 128)
-    sz = O.scales_zeros(s, z)
-    return {"packed": O.pack_nibbles_even_low(q), "sz": sz, "w_eff": O.dequant_int4_zp(q, sz, 128)}
+TIGHT = 4e-3
+CHAIN_DRIFT = 6e-2
+SHAPES = (("qkv", QKV, H), ("o", H, ATT), ("gu", 2 * MLP, H), ("dn", H, MLP))
+CHAINS = [(m, layout) for m in (1, 2) for layout in ("tiled", "rowmajor")]
 
 
-def _gamma(k, rng):
-    return O.f32_to_bf16_bits(np.float32(1.0) + rng.standard_normal(k, dtype=np.float32) * np.float32(0.1))
+def _layer(i: int, dev):
+    """Layer i's quantized weights (packed uint8, scales_zeros bf16, on the
+    GPU) and RMSNorm weights, from seed SEED + i."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED + i)
+    wq = {}
+    for name, n, k in SHAPES:
+        w = torch.randn(n, k, device=dev, generator=gen) * 0.02
+        packed, sz, _ = G.quantize_int4_device(w, 128, True, G.W_INT4_ZP)
+        wq[name] = (packed, sz)
+        del w
+    g1 = (1 + 0.1 * torch.randn(H, device=dev, generator=gen)).to(torch.bfloat16)
+    g2 = (1 + 0.1 * torch.randn(H, device=dev, generator=gen)).to(torch.bfloat16)
+    return wq, g1, g2
 
 
-def _model():
-    """Oracle-quantized weights of LAYERS layers and the head (built once)."""
-    if not _STEP:
-        rng = np.random.default_rng(2560)
-        layers = []
-        for _ in range(LAYERS):
-            layers.append({"qkv": _int4(QKV, H, rng), "o": _int4(H, ATT, rng), "gu": _int4(2 * MLP, H, rng),
-                           "dn": _int4(H, MLP, rng), "g1": _gamma(H, rng), "g2": _gamma(H, rng)})
-        head = O.f32_to_bf16_bits(rng.standard_normal((VOCAB, H), dtype=np.float32) * np.float32(0.02))
-        _STEP.update(layers=layers, head=head, gf=_gamma(H, rng),
-                     h0=O.f32_to_bf16_bits(rng.standard_normal((2, H), dtype=np.float32)))
-    return _STEP
-
-
-_ORACLE: dict = {}
-
-
-def _oracle_logits(m):
-    if m not in _ORACLE:
-        _ORACLE[m] = _oracle_chain(m)
-    return _ORACLE[m]
-
-
-def _oracle_chain(m):
-    st = _model()
-    h = O.bf16_bits_to_f32(st["h0"][:m])
-    for L in st["layers"]:
-        xn = O.rmsnorm_f32(h, O.bf16_bits_to_f32(L["g1"]))
-        qkv = O.round_bf16(O.gemv_ref(xn, L["qkv"]["w_eff"]).astype(np.float32))
-        att = qkv[:, :ATT]
-        h = O.round_bf16(O.gemv_ref(att, L["o"]["w_eff"], O.EPI_RES, h).astype(np.float32))
-        xn = O.rmsnorm_f32(h, O.bf16_bits_to_f32(L["g2"]))
-        mid = O.round_bf16(O.gemv_ref(xn, L["gu"]["w_eff"], O.EPI_SILU).astype(np.float32))
-        h = O.round_bf16(O.gemv_ref(mid, L["dn"]["w_eff"], O.EPI_RES, h).astype(np.float32))
-    xn = O.rmsnorm_f32(h, O.bf16_bits_to_f32(st["gf"]))
-    return O.gemv_ref(xn, O.bf16_bits_to_f32(st["head"]))
-
-
-def _device_weight(wq, k, layout, paired=False):
-    packed, sz = u8_tensor(wq["packed"]), bf16_tensor(wq["sz"])
+def _device_weight(packed, sz, k, layout, paired=False):
     if layout == "rowmajor":
         return {"w": packed, "wfmt": G.W_INT4_ZP, "sc0": sz, "group": 128}
     wfmt = G.W_INT4_TILED_PAIRED if paired else G.W_INT4_TILED
     return {"w": G.pack_tiled(G.W_INT4_ZP, packed, k, wfmt, sc0=sz), "wfmt": wfmt}
 
 
-def _gpu_logits(m, layout):
-    st = _model()
-    dev = torch.device("cuda", 0)
-    layers = [{"qkv": _device_weight(L["qkv"], H, layout), "o": _device_weight(L["o"], ATT, layout),
-               "gu": _device_weight(L["gu"], H, layout, paired=True), "dn": _device_weight(L["dn"], MLP, layout),
-               "g1": bf16_tensor(L["g1"]), "g2": bf16_tensor(L["g2"])} for L in st["layers"]]
-    head, gf = bf16_tensor(st["head"]), bf16_tensor(st["gf"])
-    h0 = bf16_tensor(st["h0"][:m])
-    hs = torch.empty_like(h0)
-    qkv = torch.empty(m, QKV, device=dev, dtype=torch.bfloat16)
-    att = torch.empty(m, ATT, device=dev, dtype=torch.bfloat16)
-    mid = torch.empty(m, MLP, device=dev, dtype=torch.bfloat16)
-    tiled = layout == "tiled"
-    for i, L in enumerate(layers):
-        x_in = h0 if i == 0 else hs
-        if tiled:   # the attention stand-in's copy as the QKV launch's second store
-            G.gemv(x_in, n=QKV, gamma=L["g1"], out=qkv, out2=att, **L["qkv"])
+def _w_eff(packed, sz):
+    """The oracle's W_eff from the packed bytes (bench_gemv.py:51-52)."""
+    return O.dequant_int4_zp(O.unpack_nibbles_even_low(packed.cpu().numpy()), bf16_bits(sz), 128)
+
+
+class _Chain:
+    """One GPU chain (M rows, one layout) with its activation buffers."""
+
+    def __init__(self, h0: torch.Tensor, layout: str):
+        self.m, self.layout = h0.shape[0], layout
+        dev = h0.device
+        self.h0, self.hs = h0, torch.empty_like(h0)
+        self.qkv = torch.empty(self.m, QKV, device=dev, dtype=torch.bfloat16)
+        self.att = torch.empty(self.m, ATT, device=dev, dtype=torch.bfloat16)
+        self.mid = torch.empty(self.m, MLP, device=dev, dtype=torch.bfloat16)
+
+    def layer(self, i, wq, g1, g2) -> dict:
+        """Run layer i; returns each GEMV's input and output as float32."""
+        t = {name: _device_weight(*wq[name], k, self.layout, paired=name == "gu") for name, _, k in SHAPES}
+        x_in = self.h0 if i == 0 else self.hs
+        seen = {"x_in": f32(x_in)}
+        if self.layout == "tiled":  # the attention stand-in's copy as the QKV launch's second store
+            G.gemv(x_in, n=QKV, gamma=g1, out=self.qkv, out2=self.att, **t["qkv"])
         else:
-            G.gemv(x_in, n=QKV, gamma=L["g1"], out=qkv, **L["qkv"])
-            att.copy_(qkv[:, :ATT])
-        G.gemv(att, n=H, epilogue=G.EPI_RESIDUAL, residual=x_in, out=hs, **L["o"])
-        G.gemv(hs, n=2 * MLP, gamma=L["g2"], epilogue=G.EPI_SILU_GATE, out=mid, **L["gu"])
-        G.gemv(mid, n=H, epilogue=G.EPI_RESIDUAL, residual=hs, out=hs, **L["dn"])
-    logits = G.gemv(hs, head, G.W_BF16, VOCAB, gamma=gf)
-    torch.cuda.synchronize()
-    return f32(logits)
+            G.gemv(x_in, n=QKV, gamma=g1, out=self.qkv, **t["qkv"])
+            self.att.copy_(self.qkv[:, :ATT])
+        seen["qkv"], seen["att"] = f32(self.qkv), f32(self.att)
+        G.gemv(self.att, n=H, epilogue=G.EPI_RESIDUAL, residual=x_in, out=self.hs, **t["o"])
+        seen["h"] = f32(self.hs)
+        G.gemv(self.hs, n=2 * MLP, gamma=g2, epilogue=G.EPI_SILU_GATE, out=self.mid, **t["gu"])
+        seen["mid"] = f32(self.mid)
+        G.gemv(self.mid, n=H, epilogue=G.EPI_RESIDUAL, residual=self.hs, out=self.hs, **t["dn"])
+        seen["out"] = f32(self.hs)
+        return seen
+
+    def logits(self, head, gf):
+        return f32(G.gemv(self.hs, head, G.W_BF16, VOCAB, gamma=gf))
 
 
-@pytest.mark.parametrize("layout", ["tiled", "rowmajor"])
-@pytest.mark.parametrize("m", [1, 2])
-def test_c5_step_logits_match_oracle(m, layout):
-    got = _gpu_logits(m, layout)
-    ref = _oracle_logits(m)
-    assert got.shape == (m, VOCAB)
-    err = O.rel_err(got, ref)
-    assert err <= TOL, err
+def _split(rows, sizes):
+    out, r0 = [], 0
+    for n in sizes:
+        out.append(rows[r0:r0 + n])
+        r0 += n
+    return out
+
+
+def test_c5_full_step_26_layers_matches_oracle():
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(SEED)
+    h0 = O.f32_to_bf16_bits(rng.standard_normal((2, H), dtype=np.float32))
+    chains = {key: _Chain(bf16_tensor(h0[:key[0]]), key[1]) for key in CHAINS}
+    sizes = [m for m, _ in CHAINS]
+    worst = {}
+
+    def check(name, got_rows, ref_rows, bar):
+        for key, got, ref in zip(CHAINS, got_rows, _split(ref_rows, sizes)):
+            e = O.rel_err(got, ref)
+            worst[(name, bar)] = max(worst.get((name, bar), 0.0), e)
+            assert e <= bar, (name, key, bar, e)
+
+    chain_h = O.bf16_bits_to_f32(h0)   # the oracle's own 26-layer chain (2 rows)
+    for i in range(LAYERS):
+        wq, g1, g2 = _layer(i, dev)
+        seen = [chains[key].layer(i, wq, g1, g2) for key in CHAINS]
+        torch.cuda.synchronize()
+        weff = {name: _w_eff(*wq[name]) for name, _, _ in SHAPES}
+        g1f, g2f = O.bf16_bits_to_f32(bf16_bits(g1)), O.bf16_bits_to_f32(bf16_bits(g2))
+        del wq
+        cat = {k: np.concatenate([s[k] for s in seen]) for k in seen[0]}
+        n = len(cat["x_in"])
+        # each GEMV on the chains' own inputs (teacher-forced rows), the
+        # reference semantics, and the oracle chain's next step, in one product
+        r = O.gemv_ref(np.concatenate([O.rmsnorm_folded(cat["x_in"], g1f), O.rmsnorm_f32(cat["x_in"], g1f),
+                                       O.rmsnorm_folded(chain_h, g1f)]), weff["qkv"])
+        check("qkv", [s["qkv"] for s in seen], r[:n], TIGHT)
+        check("qkv", [s["qkv"] for s in seen], r[n:2 * n], TOL)
+        chain_att = O.round_bf16(r[2 * n:].astype(np.float32))[:, :ATT]
+        r = O.gemv_ref(np.concatenate([cat["att"], chain_att]), weff["o"], O.EPI_RES,
+                       np.concatenate([cat["x_in"], chain_h]))
+        check("o_proj", [s["h"] for s in seen], r[:n], TIGHT)
+        chain_h = O.round_bf16(r[n:].astype(np.float32))
+        r = O.gemv_ref(np.concatenate([O.rmsnorm_folded(cat["h"], g2f), O.rmsnorm_f32(cat["h"], g2f),
+                                       O.rmsnorm_folded(chain_h, g2f)]), weff["gu"], O.EPI_SILU)
+        check("gate|up", [s["mid"] for s in seen], r[:n], TIGHT)
+        check("gate|up", [s["mid"] for s in seen], r[n:2 * n], TOL)
+        chain_mid = O.round_bf16(r[2 * n:].astype(np.float32))
+        r = O.gemv_ref(np.concatenate([cat["mid"], chain_mid]), weff["dn"], O.EPI_RES,
+                       np.concatenate([cat["h"], chain_h]))
+        check("down", [s["out"] for s in seen], r[:n], TIGHT)
+        chain_h = O.round_bf16(r[n:].astype(np.float32))
+        del weff
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED + LAYERS)
+    head = (torch.randn(VOCAB, H, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+    gf = (1 + 0.1 * torch.randn(H, device=dev, generator=gen)).to(torch.bfloat16)
+    gff, headf = O.bf16_bits_to_f32(bf16_bits(gf)), f32(head)
+    finals = [f32(chains[key].hs) for key in CHAINS]
+    logits = [chains[key].logits(head, gf) for key in CHAINS]
+    last = np.concatenate(finals)
+    r = O.gemv_ref(np.concatenate([O.rmsnorm_folded(last, gff), O.rmsnorm_f32(last, gff),
+                                   O.rmsnorm_folded(chain_h, gff)]), headf)
+    n = len(last)
+    check("head", logits, r[:n], TIGHT)
+    check("head", logits, r[n:2 * n], TOL)
+    chain_logits = r[2 * n:]
+    assert np.isfinite(chain_logits).all() and np.abs(chain_logits).max() > 0
+    drift = {key: O.rel_err(lg, chain_logits[:key[0]]) for key, lg in zip(CHAINS, logits)}
+    print(f"worst per-GEMV errors over {LAYERS} layers: "
+          + ", ".join(f"{k[0]}@{k[1]:g} {v:.2e}" for k, v in sorted(worst.items())), flush=True)
+    print("end-to-end logits drift against the oracle chain: "
+          + ", ".join(f"M{m} {lay} {d:.2e}" for (m, lay), d in drift.items()), flush=True)
+    for key, d in drift.items():
+        assert d <= CHAIN_DRIFT, (key, d)

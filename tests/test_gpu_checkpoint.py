@@ -85,6 +85,36 @@ def test_rowmajor_checkpoint_is_retiled_on_load(tmp_path):
     assert torch.equal(fresh(x), ref)
 
 
+def test_reference_fp8_checkpoint_is_retiled_on_load(tmp_path):
+    """A checkpoint of the reference's Fp8Linear buffers -- row-major [N, K]
+    codes, no layout tag in its manifest entries -- loads onto the GPU
+    re-tiled: the bytes of a module quantized here, the same outputs."""
+    torch.manual_seed(2)
+    model = _MLP().to("cuda", torch.bfloat16)
+    F8.quantize_module_fp8(model, min_bytes=0)
+    x = torch.randn(2, 512, device="cuda").to(torch.bfloat16)
+    ref = model(x)
+    tiled = {n: getattr(model, n).weight_fp8.view(torch.uint8).clone() for n in ("gate_proj", "up_proj", "down_proj")}
+    for name, w in tiled.items():
+        mod = getattr(model, name)
+        codes, _ = O.untile_fp8(w.cpu().numpy().reshape(-1), mod.out_features, mod.in_features)
+        mod.weight_fp8 = torch.from_numpy(codes).cuda().view(torch.float8_e4m3fn)
+    man = Q.save_quantized(model, tmp_path, {}, source="synthetic")
+    assert {e["layout"] for e in man["modules"].values()} == {F8.LAYOUT_ROWMAJOR}
+    for e in man["modules"].values():   # as the reference writes it: no layout tag
+        del e["layout"]
+    (tmp_path / Q.MANIFEST_NAME).write_text(__import__("json").dumps(man))
+    fresh = _MLP()
+    Q.install_shells(fresh, Q.read_manifest(tmp_path), "meta")
+    Q.load_quantized_state(fresh, tmp_path, "cuda")
+    for name, w in tiled.items():
+        assert F8.layout_of(getattr(fresh, name).weight_fp8, w.shape[0] * 16, 0) == F8.LAYOUT_TILED
+        assert torch.equal(getattr(fresh, name).weight_fp8.view(torch.uint8), w), name
+    assert torch.equal(fresh(x), ref)
+    man2 = Q.save_quantized(fresh, tmp_path / "again", {}, source="synthetic")
+    assert {e["layout"] for e in man2["modules"].values()} == {F8.LAYOUT_TILED}
+
+
 def test_module_from_logical_nibbles_matches_oracle():
     rng = np.random.default_rng(4)
     N, K = 512, 1024

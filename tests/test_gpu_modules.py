@@ -191,21 +191,75 @@ def test_int4_linear_rebuilt_from_buffers():
     assert torch.equal(mod(x), ref(x))
 
 
+def _fp8_codes(mod):
+    """(codes uint8 [N, K], scales [N]) of an Fp8Linear in either layout."""
+    if F8.layout_of(mod.weight_fp8, mod.out_features, mod.in_features) == F8.LAYOUT_ROWMAJOR:
+        return mod.weight_fp8.view(torch.uint8).cpu().numpy(), mod.weight_scale.cpu().numpy()[0]
+    return O.untile_fp8(mod.weight_fp8.view(torch.uint8).cpu().numpy().reshape(-1), mod.out_features,
+                        mod.in_features)
+
+
 def test_fp8_linear_buffers_and_forward():
+    """A tileable shape: weight_fp8 holds the tiled bytes (the oracle's tiling
+    of the reference-formula codes and scales, byte for byte), weight_scale
+    the reference's (1, N) scales; forward runs the tiled GEMV paths and, past
+    32 rows, the chunked dequantize-then-GEMM."""
     N, K = 320, 768
     lin, w = _linear(N, K, 22, "cuda")
     mod = F8.Fp8Linear(lin)
-    assert mod.weight_fp8.dtype == torch.float8_e4m3fn and tuple(mod.weight_fp8.shape) == (N, K)
+    assert mod.weight_fp8.dtype == torch.float8_e4m3fn
+    assert tuple(mod.weight_fp8.shape) == F8.tiled_shape(N, K) == (N // 16, 16 * K + 128)
+    assert F8.layout_of(mod.weight_fp8, N, K) == F8.LAYOUT_TILED
     assert mod.weight_scale.dtype == torch.float32 and tuple(mod.weight_scale.shape) == (1, N)
     codes, scale = O.quantize_fp8_linear(w)
-    assert np.array_equal(mod.weight_fp8.view(torch.uint8).cpu().numpy(), codes)
+    assert np.array_equal(mod.weight_fp8.view(torch.uint8).cpu().numpy().reshape(-1), O.tile_fp8(codes, scale))
     assert np.array_equal(mod.weight_scale.cpu().numpy()[0], scale)
-    for M in (3, 12, 40):  # row-sliced path, tile kernel, tile kernel in two launches
+    for M in (1, 2, 3, 12, 40):  # streaming, panel, chunked dequantize-then-GEMM
         x = torch.randn(M, K, device=_dev()).to(torch.bfloat16)
         y = mod(x)
         assert y.dtype == torch.bfloat16 and tuple(y.shape) == (M, N)
         ref = O.gemv_ref(x.float().cpu().numpy(), O.dequant_fp8(codes, scale))
         assert O.rel_err(f32(y), ref) <= TOL, M
+
+
+def test_fp8_linear_rowmajor_buffers_retile():
+    """A module holding the reference's row-major buffers (as its checkpoints
+    do) gives the same outputs before and after retile(), which turns it into
+    the tiled module's bytes."""
+    N, K = 256, 1024
+    lin, w = _linear(N, K, 23, "cuda")
+    tiled = F8.Fp8Linear(lin)
+    codes, scale = O.quantize_fp8_linear(w)
+    mod = F8.Fp8Linear.__new__(F8.Fp8Linear)
+    nn.Module.__init__(mod)
+    mod.in_features, mod.out_features = K, N
+    mod.register_buffer("weight_fp8", u8_tensor(codes).view(torch.float8_e4m3fn))
+    mod.register_buffer("weight_scale", torch.from_numpy(scale.reshape(1, N).copy()).to(_dev()))
+    x = torch.randn(2, K, device=_dev()).to(torch.bfloat16)
+    before = mod(x)
+    assert O.rel_err(f32(before), O.gemv_ref(x.float().cpu().numpy(), O.dequant_fp8(codes, scale))) <= TOL
+    assert F8.retile(mod) and not F8.retile(mod)
+    assert torch.equal(mod.weight_fp8.view(torch.uint8), tiled.weight_fp8.view(torch.uint8))
+    assert torch.equal(mod(x), tiled(x))
+
+
+@pytest.mark.parametrize("mod_kind", ["int4", "fp8"])
+def test_prefill_rows_chunked(mod_kind):
+    """More than 32 rows: the weight is decoded in runs of whole 16-row blocks
+    (a 1 MiB fp32 budget here forces several runs, one of them short) and
+    multiplied by the library GEMM; the result equals the one-run product."""
+    N, K, M = 400, 1280, 48
+    lin, w = _linear(N, K, 24, "cuda")
+    mod = I4.Int4Linear(lin) if mod_kind == "int4" else F8.Fp8Linear(lin)
+    buf = mod.weight_int4 if mod_kind == "int4" else mod.weight_fp8.view(torch.uint8)
+    wfmt = G.W_INT4_TILED if mod_kind == "int4" else G.W_FP8_TILED
+    x = torch.randn(M, K, device=_dev()).to(torch.bfloat16)
+    small = G.dequant_matmul(x, buf, wfmt, N, K, chunk_bytes=1 << 20)   # 192-row runs: 192 + 192 + 16
+    whole = G.dequant_matmul(x, buf, wfmt, N, K, chunk_bytes=1 << 30)
+    assert torch.equal(small, whole)
+    assert torch.equal(mod(x), whole)
+    w_eff = f32(G.dequant(wfmt, buf, N, K))
+    assert O.rel_err(f32(whole), O.gemv_ref(x.float().cpu().numpy(), w_eff)) <= TOL
 
 
 class _Mlp(nn.Module):
@@ -255,8 +309,8 @@ def test_quantize_module_fp8_converts_large_layers():
     nbytes = 2048 * 1536 * 4
     assert stats == {"converted": 3, "skipped_below_threshold": 0, "weight_bytes_saved": 3 * (nbytes // 2)}
     got = m(x)
-    wd = {n: G.dequant(G.W_FP8, getattr(m, n).weight_fp8.view(torch.uint8), getattr(m, n).out_features,
-                       getattr(m, n).in_features, sc0=getattr(m, n).weight_scale)
+    wd = {n: G.dequant(G.W_FP8_TILED, getattr(m, n).weight_fp8.view(torch.uint8), getattr(m, n).out_features,
+                       getattr(m, n).in_features)
           for n in ("gate_proj", "up_proj", "down_proj")}
     h = torch.nn.functional.silu(x @ wd["gate_proj"].t()) * (x @ wd["up_proj"].t())
     assert O.rel_err(f32(got), f32(h @ wd["down_proj"].t())) <= TOL
@@ -342,8 +396,8 @@ def test_from_fp8_concat(paired):
     mods = [F8.Fp8Linear(_linear(n, K, 50 + i, "cuda")[0]) for i, n in enumerate(sizes)]
     fw = FK.FusedWeight.from_fp8(*mods, paired=paired)
     assert fw.N == sum(sizes) and fw.layout == ("tiled-paired" if paired else "tiled")
-    codes = np.concatenate([m.weight_fp8.view(torch.uint8).cpu().numpy() for m in mods])
-    scale = np.concatenate([m.weight_scale.cpu().numpy()[0] for m in mods])
+    codes = np.concatenate([_fp8_codes(m)[0] for m in mods])
+    scale = np.concatenate([_fp8_codes(m)[1] for m in mods])
     assert np.array_equal(fw.w.cpu().numpy(), O.tile_fp8(codes, scale, paired=paired))
     x = torch.randn(1, K, device=_dev()).to(torch.bfloat16)
     if paired:
