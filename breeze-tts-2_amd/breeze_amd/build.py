@@ -44,7 +44,8 @@ HIP_FLAGS = [
 # access.  Patterns over the mangled names; the attention kernel's bf16-cache
 # instances with D <= 256 (attn_kernel<DL = 1, 2, 4, GM, F32C = false, ...>)
 # are covered, its fp32-cache and D = 512 instances are allowed scratch.
-NO_SCRATCH = (r"gemv_persist", r"gemv_mfma", r"gemv_i8mma", r"gemv_tile", r"gemv_stream", r"gemv_panel", r"head_f32", r"qkv_rope_cache",
+NO_SCRATCH = (r"gemv_persist", r"gemv_mfma", r"gemv_i8mma", r"gemv_tile", r"gemv_stream", r"gemv_wide", r"gemv_panel",
+              r"head_f32", r"qkv_rope_cache",
               r"attn_kernelILi[124]ELi\d+ELb0E")
 
 

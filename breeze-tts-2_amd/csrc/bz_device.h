@@ -115,6 +115,20 @@ __device__ __forceinline__ float max16_dpp(float v) {
     return fmaxf(v, dpp_f32<kDppRowMirror>(v));
 }
 
+// Sum of the four 16-lane rows of a wave once each row holds its own sum
+// (after sum16_dpp): GFX9's DPP row broadcasts add row 0 into row 1 and row 2
+// into row 3 (row_bcast:15), then lane 31 into rows 2 and 3 (row_bcast:31);
+// lane 63 gets (r3 + r2) + (r1 + r0).  Two VALU operations, no LDS.
+constexpr int kDppRowBcast15 = 0x142;
+constexpr int kDppRowBcast31 = 0x143;
+__device__ __forceinline__ float rows4_sum_lane63(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kDppRowBcast15, 0xA, 0xF,
+                                                               false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kDppRowBcast31, 0xC, 0xF,
+                                                               false));
+    return v;
+}
+
 // Sum over each aligned quad of lanes.
 __device__ __forceinline__ float sum4(float v) {
     v += dpp_f32<kDppXor1>(v);

@@ -9,6 +9,7 @@
 
 #include "bz_gemv_panel.h"
 #include "bz_gemv_tile.h"
+#include "bz_gemv_wide.h"
 
 namespace bz {
 
@@ -265,17 +266,108 @@ static int launch_stream(int wf, const StreamParams& p, const StreamLaunch& l, h
     }
 }
 
+static int launch_wide(int wf, const StreamParams& p, const WideLaunch& l, int nblk, hipStream_t st) {
+    switch (wf) {
+        case WF_I4T: return launch_wide_i4t(p, l, nblk, st);
+        case WF_I4TP: return launch_wide_i4tp(p, l, nblk, st);
+        case WF_F8T: return launch_wide_f8t(p, l, nblk, st);
+        case WF_F8TP: return launch_wide_f8tp(p, l, nblk, st);
+        default: return BZ_ERR_INVALID_ARG;
+    }
+}
+
+// Launch shape of the several-block kernel (bz_gemv_wide.h) for `rows` rows
+// of x (<= 8) and T row blocks per workgroup.  Waves: about 2 units each for
+// int4, 5 for fp8 over several blocks and 8 for fp8 over one, at most 16.
+// Measured on MI355X at M = 1 (kernel time, weights rotated through 1 GiB):
+// int4 gate|up K2560 N20480, 5 blocks per workgroup: 10 x 2 7.08 us, 7 x 3
+// 7.06, 5 x 4 7.51; int4 qkv K2560 N6144, 2 blocks: 10 x 2 4.11, 7 x 3 4.34,
+// 5 x 4 4.52; fp8 gate|up, 5 blocks: 8 x 5 10.05, 10 x 4 10.11, 7 x 6 10.75;
+// fp8 o_proj K4096 N2560, 1 block: 8 x 8 4.13, 16 x 4 4.15.
+static int wide_plan(const bz_gemv_desc* d, int rows, int T, WideLaunch& l) {
+    l.upw = 0;  // stays 0 when no unit count fits (the caller tells that apart from an LDS overflow)
+    const int wf = d->wfmt;
+    const int NU = tiled_units(wf, d->K), nblk = d->N / 16;
+    if (T < 1 || T > kWideMaxBlocks) return BZ_ERR_INVALID_ARG;
+    int nw = d->cfg_waves;
+    if (nw < 0 || nw > kStreamMaxWaves) return BZ_ERR_INVALID_ARG;
+    const int per_wave = tiled_i4(wf) ? 2 : T > 1 ? 5 : 8;
+    if (!nw) nw = std::min(kStreamMaxWaves, (NU + per_wave - 1) / per_wave);
+    const int need = (NU + nw - 1) / nw;
+    const int mm = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+    int upw = 0;
+    for (int u : kWideUpw)
+        if (u >= need && u <= wide_max_upw(wf, 1)) {
+            upw = u;
+            break;
+        }
+    if (!upw) return BZ_ERR_UNSUPPORTED;  // K too long for the waves
+    l.upw = upw;
+    if (upw > wide_max_upw(wf, mm)) return BZ_ERR_UNSUPPORTED;  // fits over fewer rows of x
+    nw = std::min(nw, (NU + upw - 1) / upw);  // every wave owns at least one unit
+    l.nw = nw;
+    l.mm = mm;
+    l.T = T;
+    l.grid = (unsigned)((nblk + T - 1) / T);
+    l.lds = (size_t)wide_lds(wf, rows, d->K, T).total;
+    return l.lds <= (size_t)device_lds_limit() ? BZ_OK : BZ_ERR_UNSUPPORTED;
+}
+
+// Row blocks per workgroup the rule gives the several-block kernel, 0 for
+// the one-block streaming kernel:
+//   * more row blocks than the 256 CUs: enough blocks per workgroup for one
+//     workgroup per CU (gate|up N = 20480: 5; qkv N = 6144: 2).  Measured on
+//     MI355X at M = 1 against the one-block kernel: int4 gate|up 7.59 ->
+//     7.08 us, int4 qkv 4.54 -> 4.11 us, fp8 gate|up 10.52 -> 10.05 us;
+//   * fp8 rows of 64 units or more (K >= 4096) over at most 256 blocks: one
+//     block per workgroup, all its tiles in flight behind the x loads (fp8
+//     down K10240 N2560 7.43 -> 7.18 us, fp8 o_proj K4096 N2560 4.38 -> 4.13).
+//     Not fp8 qkv K2560 N4096 (one-block 3.92 us, several-block 4.02) nor the
+//     int4 rows of at most 256 blocks (int4 down K10240 N2560 5.69 against
+//     5.74, o_proj K4096 3.77 both).
+static int wide_rule(const bz_gemv_desc* d) {
+    const int nblk = d->N / 16, NU = tiled_units(d->wfmt, d->K);
+    if (nblk > 256) return std::min(kWideMaxBlocks, (nblk + 255) / 256);
+    if (!tiled_i4(d->wfmt) && NU >= 64) return 1;
+    return 0;
+}
+
+// The streaming kernel a tiled descriptor runs on and its launch shape: the
+// rule's choice without a cfg; on path 5 forced, cfg_tiles = 0 the one-block
+// kernel and cfg_tiles >= 1 the several-block kernel with that many blocks
+// per workgroup (cfg_waves waves, 0 = the kernel's own rule, either way).
+struct TiledPlan {
+    bool wide;
+    StreamLaunch s;
+    WideLaunch w;
+};
+
+static int tiled_plan(const bz_gemv_desc* d, int rows, TiledPlan& pl) {
+    int T;
+    if (d->cfg_path == PATH_STREAM) {
+        if (d->cfg_tiles < 0 || d->cfg_tiles > kWideMaxBlocks) return BZ_ERR_INVALID_ARG;
+        T = d->cfg_tiles;
+    } else {
+        T = wide_rule(d);
+        // a row too long for the several-block kernel's waves (int4 beyond
+        // 16 x 5 units) stays on the one-block kernel
+        if (T && wide_plan(d, rows, T, pl.w) == BZ_ERR_UNSUPPORTED && pl.w.upw == 0) T = 0;
+    }
+    pl.wide = T > 0;
+    return pl.wide ? wide_plan(d, rows, T, pl.w) : stream_plan(d, rows, pl.s);
+}
+
 // The tiled formats: up to kStreamMaxRows rows per launch (fewer when their
 // staged x does not fit the LDS), each launch streaming the weights once.
 static int gemv_tiled(const bz_gemv_desc* d, const DescInfo& di, hipStream_t st) {
     const int M = d->M;
     int rows = std::min(M, kStreamMaxRows);
-    StreamLaunch l{};
-    int rc = stream_plan(d, rows, l);
-    while (rc == BZ_ERR_UNSUPPORTED && rows > 1 && l.upw) rc = stream_plan(d, --rows, l);
+    TiledPlan pl{};
+    int rc = tiled_plan(d, rows, pl);
+    while (rc == BZ_ERR_UNSUPPORTED && rows > 1 && (pl.wide ? pl.w.upw : pl.s.upw)) rc = tiled_plan(d, --rows, pl);
     if (rc != BZ_OK) return rc;
-    StreamLaunch l_rem = l;  // the last, shorter launch (planned before anything is launched)
-    if (M > rows && M % rows && stream_plan(d, M % rows, l_rem) != BZ_OK) return BZ_ERR_UNSUPPORTED;
+    TiledPlan pl_rem = pl;  // the last, shorter launch (planned before anything is launched)
+    if (M > rows && M % rows && tiled_plan(d, M % rows, pl_rem) != BZ_OK) return BZ_ERR_UNSUPPORTED;
     StreamParams p{};
     p.ldx = d->ldx;
     p.w = static_cast<const uint8_t*>(d->w);
@@ -297,13 +389,13 @@ static int gemv_tiled(const bz_gemv_desc* d, const DescInfo& di, hipStream_t st)
     const size_t osz = p.out_f32 ? 4 : 2, rsz = p.res_f32 ? 4 : 2;
     for (int m0 = 0; m0 < M; m0 += rows) {
         const int r = std::min(rows, M - m0);
-        const StreamLaunch& q = r == rows ? l : l_rem;
+        const TiledPlan& q = r == rows ? pl : pl_rem;
         p.M = r;
         p.x = static_cast<const uint16_t*>(d->x) + (int64_t)m0 * d->ldx;
         p.out = static_cast<uint8_t*>(d->out) + (int64_t)m0 * d->ldo * osz;
         p.out2 = d->n_out2 ? static_cast<uint8_t*>(d->out2) + (int64_t)m0 * d->ldo2 * osz : nullptr;
         p.res = d->residual ? static_cast<const uint8_t*>(d->residual) + (int64_t)m0 * d->ldr * rsz : nullptr;
-        const int lrc = launch_stream(d->wfmt, p, q, st);
+        const int lrc = q.wide ? launch_wide(d->wfmt, p, q.w, d->N / 16, st) : launch_stream(d->wfmt, p, q.s, st);
         if (lrc != BZ_OK) return lrc;
     }
     return BZ_OK;

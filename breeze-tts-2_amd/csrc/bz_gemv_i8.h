@@ -304,15 +304,7 @@ __global__ void __launch_bounds__(kMaxThreads) gemv_i8mma(GemvParams p, int M) {
 template <int WF, int MQ, int T, int D, bool SILU>
 int launch_i8_kernel(const GemvParams& p, const Launch& l, hipStream_t st) {
     auto kern = gemv_i8mma<WF, MQ, T, D, SILU>;
-    if (l.lds > 65536) {
-        static std::atomic<bool> raised{false};
-        if (!raised.load(std::memory_order_relaxed)) {
-            if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    device_lds_limit()) != hipSuccess)
-                return BZ_ERR_LAUNCH;
-            raised.store(true, std::memory_order_relaxed);
-        }
-    }
+    if (l.lds > 65536 && raise_lds_limit(reinterpret_cast<const void*>(kern)) != BZ_OK) return BZ_ERR_LAUNCH;
     hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, p, l.M);
     return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }

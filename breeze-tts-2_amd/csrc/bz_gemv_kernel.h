@@ -55,6 +55,9 @@
 // pairs of x.
 #pragma once
 #include <atomic>
+#include <mutex>
+#include <set>
+#include <utility>
 
 #include "bz_device.h"
 #include "bz_gemv.h"
@@ -679,6 +682,25 @@ inline int device_lds_limit() {
     return lim;
 }
 
+// Raise a kernel's dynamic-LDS limit to the device's maximum, once per
+// (device, kernel): hipFuncSetAttribute acts on the current device only, so
+// a kernel first launched on one GPU still needs it on the next.
+inline int raise_lds_limit(const void* kern) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return BZ_ERR_LAUNCH;
+    static std::mutex mu;
+    static std::set<std::pair<int, const void*>> done;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        if (done.count({dev, kern})) return BZ_OK;
+    }
+    if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, device_lds_limit()) != hipSuccess)
+        return BZ_ERR_LAUNCH;
+    std::lock_guard<std::mutex> lock(mu);
+    done.insert({dev, kern});
+    return BZ_OK;
+}
+
 struct Launch {
     int M, depth, nw;
     bool silu;
@@ -692,15 +714,7 @@ constexpr int kMaxLoadsInFlight = 16;
 template <int WF, int M, int T, int D, bool SILU>
 int launch_persist(const GemvParams& p, const Launch& l, hipStream_t st) {
     auto kern = gemv_persist<WF, M, T, D, SILU>;
-    if (l.lds > 65536) {
-        static std::atomic<bool> raised{false};
-        if (!raised.load(std::memory_order_relaxed)) {
-            if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    device_lds_limit()) != hipSuccess)
-                return BZ_ERR_LAUNCH;
-            raised.store(true, std::memory_order_relaxed);
-        }
-    }
+    if (l.lds > 65536 && raise_lds_limit(reinterpret_cast<const void*>(kern)) != BZ_OK) return BZ_ERR_LAUNCH;
     hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, p);
     return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }

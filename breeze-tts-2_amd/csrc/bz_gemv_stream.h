@@ -429,15 +429,7 @@ struct StreamLaunch {
 template <int WF, int MM, int UPW>
 int launch_stream_kernel(const StreamParams& p, const StreamLaunch& l, hipStream_t st) {
     auto kern = gemv_stream<WF, MM, UPW>;
-    if (l.lds > 65536) {
-        static std::atomic<bool> raised{false};
-        if (!raised.load(std::memory_order_relaxed)) {
-            if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    device_lds_limit()) != hipSuccess)
-                return BZ_ERR_LAUNCH;
-            raised.store(true, std::memory_order_relaxed);
-        }
-    }
+    if (l.lds > 65536 && raise_lds_limit(reinterpret_cast<const void*>(kern)) != BZ_OK) return BZ_ERR_LAUNCH;
     hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, p);
     return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }

@@ -441,15 +441,7 @@ __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
 template <int WF, int MB, int T, int D>
 int launch_tile_kernel(const TileParams& tp, const TileLaunch& l, hipStream_t st) {
     auto kern = gemv_tile<WF, MB, T, D>;
-    if (l.lds > 65536) {
-        static std::atomic<bool> raised{false};
-        if (!raised.load(std::memory_order_relaxed)) {
-            if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    device_lds_limit()) != hipSuccess)
-                return BZ_ERR_LAUNCH;
-            raised.store(true, std::memory_order_relaxed);
-        }
-    }
+    if (l.lds > 65536 && raise_lds_limit(reinterpret_cast<const void*>(kern)) != BZ_OK) return BZ_ERR_LAUNCH;
     hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, tp);
     return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }

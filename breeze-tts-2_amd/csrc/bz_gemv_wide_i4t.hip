@@ -1,0 +1,8 @@
+// Instances of the several-block streaming GEMV for one weight format (WF_I4T).
+#include "bz_gemv_wide.h"
+
+namespace bz {
+int launch_wide_i4t(const StreamParams& p, const WideLaunch& l, int nblk, hipStream_t st) {
+    return launch_wide_wf<WF_I4T>(p, l, nblk, st);
+}
+}  // namespace bz

@@ -123,9 +123,13 @@ typedef enum bz_dtype {
  * for int4 weights, group >= 128 and K % 128 == 0, x held as two int8
  * planes per row (about 16 significant bits), up to 16 rows per launch;
  * 4 = several-row bf16 MFMA tile kernel, see below; 5 = the streaming
- * kernel of the tiled formats: there cfg_waves alone is read, 1..16 waves
- * per row block; 6 = the several-row panel kernel of the tiled formats, see
- * below).
+ * kernels of the tiled formats: cfg_tiles = 0 the one-block kernel (one
+ * 16-row block per workgroup), cfg_tiles = 1..8 the several-block kernel
+ * with that many consecutive row blocks per workgroup, cfg_waves 1..16
+ * waves per workgroup (0 = the kernel's rule), cfg_depth unused; 6 = the
+ * several-row panel kernel of the tiled formats, see below).  Without a cfg
+ * the rule takes the several-block kernel for weights of more than 256 row
+ * blocks (one workgroup per CU) and for fp8 rows of 80 units or more.
  * Used by tuning sweeps.
  *
  * Several rows (path 4).  Up to 32 rows of x per launch stream every weight

@@ -508,3 +508,84 @@ def test_shared_read_reads_x_and_own_chunk():
         assert sink.tolist() == [key, 7, 7, 7]
     with pytest.raises(ValueError):
         G.shared_read(x, w, 8192, 5, sink)      # w shorter than 5 chunks
+
+
+# ---------------------------------------------------------------------------
+# the several-block streaming kernel (path 5 with cfg_tiles = blocks per
+# workgroup; the rule's choice for weights of more than 256 row blocks)
+# ---------------------------------------------------------------------------
+
+WIDE = [
+    # (fmt, n, k, norm, epilogue, blocks per workgroup)
+    ("int4", 2048, 2560, True, 1, 5),     # paired, 128 blocks / 5: a ragged last workgroup (3 blocks)
+    ("int4", 1536, 1024, False, 2, 3),
+    ("int4", 768, 4096, True, 0, 8),      # 48 blocks / 8
+    ("int4", 512, 10240, False, 0, 2),    # 80 units: 16 waves x 5
+    ("fp8", 2048, 2560, True, 1, 5),
+    ("fp8", 1024, 10240, False, 2, 1),    # one block per workgroup, all tiles in flight
+    ("fp8", 1280, 1024, True, 0, 7),
+]
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 9])
+@pytest.mark.parametrize("fmt,n,k,norm,epi,T", WIDE, ids=[f"{w[0]}-n{w[1]}-k{w[2]}-e{w[4]}-T{w[5]}" for w in WIDE])
+def test_gemv_wide_matches_oracle_and_one_block_kernel(fmt, n, k, norm, epi, T, m):
+    seed = 700 + T + m + k // 1024
+    c = _int4_case(n, k, seed) if fmt == "int4" else _fp8_case(n, k, seed)
+    buf, tf = _tiled_i4(c, epi == 1) if fmt == "int4" else _tiled_f8(c, epi == 1)
+    w_eff = c.w_zp if fmt == "int4" else c.w_eff
+    x_bits = _x(m, k, seed + 1)
+    gamma_bits = _gamma(k, seed + 2) if norm else None
+    n_out = n // 2 if epi == 1 else n
+    res_bits = _x(m, n_out, seed + 3) if epi == 2 else None
+    kw = dict(gamma=bf16_tensor(gamma_bits) if norm else None, epilogue=epi,
+              residual=bf16_tensor(res_bits) if res_bits is not None else None)
+    wide = G.gemv(bf16_tensor(x_bits), buf, tf, n, cfg=(0, 0, T, 5), **kw)
+    one = G.gemv(bf16_tensor(x_bits), buf, tf, n, cfg=(0, 0, 0, 5), **kw)
+    ref = _ref(x_bits, w_eff, gamma_bits, epi, res_bits)
+    assert O.rel_err(f32(wide), ref) <= TIGHT
+    # the same sums in another order (the waves' partials added in wave order
+    # rather than by a DPP tree): within one bf16 step of the one-block kernel
+    assert O.rel_err(f32(wide), f32(one)) <= ONE_BF16_STEP
+    # deterministic: a second call is bit-identical
+    assert torch.equal(G.gemv(bf16_tensor(x_bits), buf, tf, n, cfg=(0, 0, T, 5), **kw), wide)
+
+
+@pytest.mark.parametrize("waves", [4, 5, 7, 16])
+def test_gemv_wide_forced_waves_and_second_store(waves):
+    """Forced wave counts (uneven unit splits) and the second store on the
+    several-block kernel: out2 gets columns [0, n2) of the same launch."""
+    n, k, m, n2, T = 6144, 2560, 3, 4096, 2
+    c = _int4_case(n, k, 720 + waves)
+    buf, tf = _tiled_i4(c, False)
+    x, g = _x(m, k, 721), _gamma(k, 722)
+    out2 = torch.zeros(m, n2, device="cuda", dtype=torch.bfloat16)
+    got = G.gemv(bf16_tensor(x), buf, tf, n, gamma=bf16_tensor(g), out2=out2, cfg=(0, waves, T, 5))
+    assert torch.equal(out2, got[:, :n2])
+    assert O.rel_err(f32(got), _ref(x, c.w_zp, g, O.EPI_NONE, None)) <= TIGHT
+
+
+def test_gemv_wide_rule_at_full_size():
+    """The rule's automatic choice for the gate|up K2560 N20480 and the qkv
+    K2560 N6144 (more than 256 row blocks) and for fp8 rows of K >= 4096 is
+    the several-block kernel: the automatic result equals the one forced with
+    the rule's block count bit for bit."""
+    for fmt, n, k, epi, T in (("int4", 20480, 2560, 1, 5), ("fp8", 20480, 2560, 1, 5), ("int4", 6144, 2560, 0, 2),
+                              ("fp8", 2560, 4096, 0, 1), ("fp8", 2560, 10240, 0, 1)):
+        c = _int4_case(n, k, 730) if fmt == "int4" else _fp8_case(n, k, 731)
+        buf, tf = _tiled_i4(c, epi == 1) if fmt == "int4" else _tiled_f8(c, epi == 1)
+        x, g = _x(2, k, 732), _gamma(k, 733)
+        auto = G.gemv(bf16_tensor(x), buf, tf, n, gamma=bf16_tensor(g), epilogue=epi)
+        forced = G.gemv(bf16_tensor(x), buf, tf, n, gamma=bf16_tensor(g), epilogue=epi, cfg=(0, 0, T, 5))
+        assert torch.equal(auto, forced), (fmt, n)
+        w_eff = c.w_zp if fmt == "int4" else c.w_eff
+        assert O.rel_err(f32(auto), _ref(x, w_eff, g, epi, None)) <= TIGHT
+
+
+def test_gemv_wide_rejects_bad_block_counts():
+    n, k = 256, 1024
+    c = _int4_case(n, k, 740)
+    buf, tf = _tiled_i4(c, False)
+    x = bf16_tensor(_x(1, k, 741))
+    with pytest.raises(RuntimeError, match="status 1"):
+        G.gemv(x, buf, tf, n, cfg=(0, 0, 9, 5))
