@@ -189,7 +189,7 @@ def gemv(
     if out2 is not None:
         d.out2, d.ldo2, d.n_out2 = out2.data_ptr(), out2.stride(0), out2.shape[1]
     stream = _lib.stream_of(x)
-    if M >= _TILE_MIN_ROWS or cfg[3] == _PATH_TILE:
+    if M >= _TILE_MIN_ROWS or cfg[3] in (_PATH_TILE, _PATH_PANEL):
         need = _lib.lib().bz_gemv_workspace(ctypes.byref(d))
         if need:
             ws = _workspace(dev, stream, need)
@@ -287,11 +287,13 @@ def pack_tiled(src_wfmt: int, w: torch.Tensor, k: int, dst_wfmt: int, *, sc0: Op
     return out
 
 
-# The several-row tile kernel (path 4) runs from this many rows on; with more
-# than one K slice it needs a workspace (fp32 split-K partials and arrival
-# counters) that is zero-filled once and left zeroed by every call.
+# The several-row kernels (tile, path 4; panel, path 6) run from this many
+# rows on; with more than one K slice they need a workspace (fp32 split-K
+# partials and arrival counters) that is zero-filled once and left zeroed by
+# every call.
 _TILE_MIN_ROWS = 5
 _PATH_TILE = 4
+_PATH_PANEL = 6
 _GEMV_WS: dict = {}          # (device index, raw stream, capture id or None) -> int32 buffer
 _GEMV_WS_RETIRED: list = []  # outgrown workspaces: a captured graph may still point at one
 

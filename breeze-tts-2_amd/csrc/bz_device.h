@@ -175,6 +175,11 @@ __device__ __forceinline__ u32x4 buffer_ld16(__amdgpu_buffer_rsrc_t r, uint32_t 
 __device__ __forceinline__ u32x4 buffer_ld16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);
 }
+// Cache-policy operand of a buffer access with the agent-scope coherence bit
+// (sc1 on gfx950): what the compiler emits for a relaxed agent-scope atomic
+// load or store (__hip_atomic_load / __hip_atomic_store with
+// __HIP_MEMORY_SCOPE_AGENT), for 16-byte accesses that have no atomic form.
+constexpr int kCpolAgent = 16;
 __device__ __forceinline__ uint32_t buffer_ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }

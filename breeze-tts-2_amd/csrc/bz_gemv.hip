@@ -164,7 +164,7 @@ static int tile_plan(const bz_gemv_desc* d, const DescInfo& di, int M, TilePlan&
     const int UK = tile_unit_k(wf);
     if ((di.i4 && d->group < 128) || K % UK || di.row_bytes >= (1 << 24)) return BZ_ERR_UNSUPPORTED;
     // 32-bit offsets inside the kernel: x rows of a launch, a slice of partials
-    if ((int64_t)M * d->ldx >= (int64_t(1) << 31) || (int64_t)M * di.n_out >= (int64_t(1) << 31))
+    if ((int64_t)M * d->ldx >= (int64_t(1) << 31) || (int64_t)tile_part_rows(M) * di.n_out * 4 >= (int64_t(1) << 31))
         return BZ_ERR_UNSUPPORTED;
     pl.MB = (M + 15) / 16;
     pl.T = forced && d->cfg_tiles ? d->cfg_tiles : 1;
@@ -192,7 +192,7 @@ static int tile_plan(const bz_gemv_desc* d, const DescInfo& di, int M, TilePlan&
     pl.nsl = (units + upl - 1) / upl;
     pl.lds = (size_t)tile_lds_layout(M, pl.MB, pl.ks, wf).total;
     if (pl.lds > (size_t)device_lds_limit()) return BZ_ERR_UNSUPPORTED;
-    pl.ws = pl.nsl > 1 ? kTilePartOffset + (size_t)pl.nsl * M * di.n_out * 4 : 0;
+    pl.ws = pl.nsl > 1 ? kTilePartOffset + (size_t)pl.nsl * tile_part_rows(M) * di.n_out * 4 : 0;
     return BZ_OK;
 }
 
@@ -415,39 +415,66 @@ static bool panel_ok(const bz_gemv_desc* d) {
 // The automatic rule takes the panel kernel for them (measured on MI355X
 // against the streaming and tile kernels, int4 and fp8, N = 2560-20480,
 // K = 2560-10240, M = 2..32):
-//   * from 5 rows on while the x of one launch is at most 384 KB (M K <=
-//     196608): each workgroup reads all of it from L2, so beyond that the
-//     tile kernel's K slices (x read once per 128 columns) win (K = 10240 at
-//     M = 32); without the workspace the tile kernel needs, the panel kernel
-//     at any M >= 5;
+//   * from 5 rows on, with K slices when the x of a launch exceeds
+//     kPanelSliceX (K = 10240 at M = 16, 32) and the workspace they need is
+//     given (else over the whole K);
 //   * 3-4 rows of fp8 over at least 1280 row blocks (N >= 20480).
 static bool panel_auto(const bz_gemv_desc* d) {
     if (d->cfg_path || !panel_ok(d)) return false;
-    const int M = d->M, rows = std::min(M, kPanelMaxRows);
-    if (M >= 5) return (int64_t)rows * d->K <= 196608;
+    const int M = d->M;
+    if (M >= 5) return true;
     return M >= 3 && !tiled_i4(d->wfmt) && d->N / 16 >= 1280;
 }
 
+// x bytes of one launch above which the automatic rule splits K into slices
+// (every workgroup reads all of x over its K range from L2), the row blocks
+// per workgroup it takes then (int4, fp8) and the workgroups the slice count
+// aims for.  Measured on MI355X, K10240 N2560 (x of 320 / 640 KB at M = 16 /
+// 32), against the whole K and against the tile kernel's 128-column blocks
+// over 8-10 slices: int4 M = 32 2 blocks x 3 slices 12.7 us (whole K 13.9,
+// tile 13.4), M = 16 2 x 2 9.75 (10.0, 10.5); fp8 M = 32 3 blocks x 4 slices
+// 13.2 (tile 15.4), M = 16 3 x 4 10.6 (whole K 12.0).
+constexpr int64_t kPanelSliceX = 256 * 1024;
+constexpr int kPanelSliceBlocksI4 = 2, kPanelSliceBlocksF8 = 3;
+constexpr int kPanelTargetWorkgroups = 240;
+
 // Launch shape of the panel kernel (bz_gemv_panel.h) for `rows` <= 32 rows
-// of x: T row blocks per workgroup (cfg_tiles: 1 to 5; default by the
-// number of blocks), NW waves (cfg_waves; default about 5 units per wave, at
-// most 16 waves, 8 with several blocks) splitting the units UPW each.
-static int panel_plan(const bz_gemv_desc* d, int rows, PanelLaunch& l) {
+// of x: nsl K slices (cfg_slices; default 1 while the x of the launch is at
+// most kPanelSliceX, else about kPanelTargetWorkgroups workgroups in all), T
+// row blocks per workgroup (cfg_tiles: 1 to 5; default by the number of
+// blocks, or kPanelSliceBlocks* with slices), NW waves (cfg_waves; default
+// about 5 units per wave, at most 16 waves, 8 with several blocks) splitting
+// the slice's units UPW each.  `slices` > 0 overrides both the cfg and the
+// rule (1: no workspace).
+static int panel_plan(const bz_gemv_desc* d, int rows, PanelLaunch& l, int slices = 0) {
     const int wf = d->wfmt;
     if (tiled_paired(wf) || d->gamma || d->n_out2) return BZ_ERR_UNSUPPORTED;
     const int NU = tiled_units(wf, d->K);
     if (!NU) return BZ_ERR_SHAPE;
     if ((int64_t)rows * d->ldx * 2 >= (int64_t(1) << 31)) return BZ_ERR_UNSUPPORTED;  // 32-bit x offsets
     const int nblk = d->N / 16;
-    const int T = d->cfg_tiles ? d->cfg_tiles : panel_blocks(nblk);
+    if (d->cfg_slices < 0) return BZ_ERR_INVALID_ARG;
+    int nsl = slices ? slices : d->cfg_slices;
+    const bool rule_slices = !nsl && (int64_t)rows * d->K * 2 > kPanelSliceX;
+    const int T = d->cfg_tiles       ? d->cfg_tiles
+                  : rule_slices || nsl > 1 ? (tiled_i4(wf) ? kPanelSliceBlocksI4 : kPanelSliceBlocksF8)
+                                           : panel_blocks(nblk);
     bool t_ok = false;
     for (int t : kPanelBlocks) t_ok |= t == T;
     if (!t_ok) return BZ_ERR_INVALID_ARG;
+    const int groups = (nblk + T - 1) / T;
+    if (rule_slices) nsl = std::max(1, (kPanelTargetWorkgroups + groups / 2) / groups);
+    if (!nsl) nsl = 1;
+    nsl = std::min(nsl, NU);
+    const int ups = (NU + nsl - 1) / nsl;
+    nsl = (NU + ups - 1) / ups;
+    if (nsl > 1 && (groups > kTileCounters || (int64_t)nsl * rows * nblk * 16 * 4 >= (int64_t(1) << 31)))
+        return BZ_ERR_UNSUPPORTED;
     const int maxw = T == 1 ? kPanelMaxWaves : 8;
     int nw = d->cfg_waves;
     if (nw < 0 || nw > maxw) return BZ_ERR_INVALID_ARG;
-    if (!nw) nw = std::min(maxw, (NU + 4) / 5);
-    const int need = (NU + nw - 1) / nw;
+    if (!nw) nw = std::min(maxw, (ups + 4) / 5);
+    const int need = (ups + nw - 1) / nw;
     int upw = 0;
     for (int u : kPanelUpw)
         if (u >= need) {
@@ -455,13 +482,31 @@ static int panel_plan(const bz_gemv_desc* d, int rows, PanelLaunch& l) {
             break;
         }
     if (!upw) return BZ_ERR_UNSUPPORTED;  // K too long for the waves
-    l.nw = (NU + upw - 1) / upw;          // every wave owns at least one unit
+    l.nw = (ups + upw - 1) / upw;         // every wave owns at least one unit
     l.upw = upw;
     l.T = T;
     l.mt = rows > 16 ? 2 : 1;
-    l.grid = (unsigned)((nblk + T - 1) / T);
+    l.nsl = nsl;
+    l.ups = ups;
+    l.grid = (unsigned)(groups * nsl);
     l.lds = (size_t)panel_lds(l.nw, T, l.mt);
+    l.ws = nsl > 1 ? kTilePartOffset + (size_t)nsl * rows * nblk * 16 * 4 : 0;
     return l.lds <= (size_t)device_lds_limit() ? BZ_OK : BZ_ERR_UNSUPPORTED;
+}
+
+// Whether a descriptor's workspace holds `ws` bytes (16-byte aligned).
+static bool workspace_holds(const bz_gemv_desc* d, size_t ws) {
+    return !ws || (d->workspace && aligned(d->workspace, 16) && d->workspace_bytes >= ws);
+}
+
+// The panel plan of `rows` rows the call can run: the one asked for, or,
+// chosen by the rule but without the workspace its K slices need, the
+// whole-K plan.
+static int panel_plan_call(const bz_gemv_desc* d, int rows, PanelLaunch& l) {
+    int rc = panel_plan(d, rows, l);
+    if (rc != BZ_OK || workspace_holds(d, l.ws)) return rc;
+    if (d->cfg_path == PATH_PANEL && d->cfg_slices) return BZ_ERR_INVALID_ARG;  // forced slices, no workspace
+    return panel_plan(d, rows, l, 1);
 }
 
 // The panel kernel over all M rows, kPanelMaxRows per launch.
@@ -469,9 +514,9 @@ static int gemv_panel_rows(const bz_gemv_desc* d, hipStream_t st) {
     const int M = d->M;
     const int rows = std::min(M, kPanelMaxRows);
     PanelLaunch l{}, l_rem{};
-    int rc = panel_plan(d, rows, l);
+    int rc = panel_plan_call(d, rows, l);
     if (rc != BZ_OK) return rc;
-    if (M > rows && M % rows && (rc = panel_plan(d, M % rows, l_rem)) != BZ_OK) return rc;
+    if (M > rows && M % rows && (rc = panel_plan_call(d, M % rows, l_rem)) != BZ_OK) return rc;
     PanelParams p{};
     p.ldx = d->ldx;
     p.w = static_cast<const uint8_t*>(d->w);
@@ -484,11 +529,15 @@ static int gemv_panel_rows(const bz_gemv_desc* d, hipStream_t st) {
     p.epi = d->epilogue;
     p.out_f32 = d->out_dtype == BZ_DT_F32;
     p.res_f32 = d->residual_dtype == BZ_DT_F32;
+    p.cnt = static_cast<uint32_t*>(d->workspace);
+    p.part = d->workspace ? reinterpret_cast<float*>(static_cast<uint8_t*>(d->workspace) + kTilePartOffset) : nullptr;
     const size_t osz = p.out_f32 ? 4 : 2, rsz = p.res_f32 ? 4 : 2;
     for (int m0 = 0; m0 < M; m0 += rows) {
         const int r = std::min(rows, M - m0);
         const PanelLaunch& q = r == rows ? l : l_rem;
         p.M = r;
+        p.nsl = q.nsl;
+        p.ups = q.ups;
         p.x = static_cast<const uint16_t*>(d->x) + (int64_t)m0 * d->ldx;
         p.out = static_cast<uint8_t*>(d->out) + (int64_t)m0 * d->ldo * osz;
         p.res = d->residual ? static_cast<const uint8_t*>(d->residual) + (int64_t)m0 * d->ldr * rsz : nullptr;
@@ -505,6 +554,10 @@ using namespace bz;
 extern "C" size_t bz_gemv_workspace(const bz_gemv_desc* d) {
     DescInfo di;
     if (check_desc(d, di) != BZ_OK) return 0;
+    if (d->cfg_path == PATH_PANEL || panel_auto(d)) {
+        PanelLaunch l{};
+        return panel_plan(d, std::min(d->M, kPanelMaxRows), l) == BZ_OK ? l.ws : 0;
+    }
     if (d->cfg_path != PATH_TILE && !tile_auto(d)) return 0;
     TilePlan pl{};
     return tile_plan(d, di, std::min(d->M, kTileMaxRows), pl) == BZ_OK ? pl.ws : 0;

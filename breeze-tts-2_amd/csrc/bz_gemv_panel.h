@@ -1,7 +1,9 @@
 // Several-row GEMV over the tiled weight formats (GEMV path 6, the "panel"
 // kernel): up to 32 rows of x against an unpaired int4 or fp8 tiled weight,
-// every weight byte streamed once, each workgroup covering the whole K of its
-// row blocks, so there is no split-K partial, counter or workspace.
+// every weight byte streamed once.  A workgroup covers its row blocks over
+// the whole K, or over one of nsl K slices when the x of a launch is large
+// (every workgroup reads all of its K range of x from L2: 655 KB at M = 32,
+// K = 10240 is about 6.5 us of one CU's L2 bandwidth, measured on MI355X).
 //
 // Replaces, for M > 2 (MTP draft verification plus CFG):
 //   torch._weight_int4pack_mm (Int4Linear)          models/int4_linear.py:103-108
@@ -28,6 +30,13 @@
 //     T scale quads per unit) in a rolling register pipeline.
 //   * One workgroup barrier: the waves' partials go to LDS, then each thread
 //     sums its outputs' partials over the waves in wave order.
+//   * K slices (nsl > 1): the grid is (row-block groups) x nsl, the slices of
+//     one group consecutive.  Each workgroup stores its fp32 sums to the
+//     workspace ([nsl][M][N] after kTileCounters counters, agent-scope
+//     stores that reach the point of coherence), waits for its stores and
+//     counts its arrival on the group's counter; the last arrival sums the
+//     slices in slice order (independent of the arrival order), applies the
+//     epilogue and resets the counter to zero for the next call.
 //
 // Arithmetic: v_mfma_f32_16x16x32_bf16 with A = 16 weight rows (lane l holds
 // 16 bytes of tile row l % 16 at byte 16 (l / 16) of the unit, which is the
@@ -62,6 +71,9 @@ struct PanelParams {
     int64_t ldo;
     int M, K, NU, nblk;
     int epi, out_f32, res_f32;
+    int nsl, ups;    // K slices and units per slice (nsl = 1: ups = NU)
+    uint32_t* cnt;   // nsl > 1: per-group arrival counters (zero between calls)
+    float* part;     // nsl > 1: fp32 sums [nsl][M][nblk * 16]
 };
 
 // Rows of x one launch takes, and the most waves of a workgroup.
@@ -77,14 +89,15 @@ constexpr int kPanelBlocks[] = {1, 2, 3, 4, 5};
 // one row half).  fp8 with two row halves and several blocks keeps two:
 // measured on MI355X, K2560 N20480 M = 32 14.1 -> 13.4 us (184 VGPRs, no
 // spills), while two units made int4 K2560 N20480 at M = 8 / 16 and fp8 at
-// M = 16 0.1-1.3 us slower.
+// M = 16 0.1-1.3 us slower, and int4 K10240 N2560 M = 32 over 2 blocks and 3
+// K slices 12.7 -> 13.6 us.
 __host__ __device__ constexpr int panel_depth(bool i4, int mt, int t, int upw) {
     return (i4 ? (t > 1 || mt == 2) : (t > 1 && mt == 1)) ? 1 : (upw <= 2 ? upw : 2);
 }
 
 // LDS: the waves' partials [wave][block][row half][x row % 16][weight row],
-// fp32.
-__host__ __device__ inline int panel_lds(int NW, int T, int MT) { return NW * T * MT * 256 * 4; }
+// fp32, then the last-arrival flag.
+__host__ __device__ inline int panel_lds(int NW, int T, int MT) { return NW * T * MT * 256 * 4 + 16; }
 
 // Lane g = l / 16 of a wave's 16-lane rows holds 16-byte piece g of its
 // weight row (dwords M[g][0..3]).  An MFMA whose four lane rows hold one
@@ -121,9 +134,12 @@ __global__ void __launch_bounds__(T == 1 ? 1024 : 512) gemv_panel(PanelParams p)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 15, kq = lane >> 4;
-    const int M = p.M, NU = p.NU;
-    const int blk0 = blockIdx.x * T;
-    const int u0 = wave * UPW;
+    const int M = p.M;
+    const int grp = (int)blockIdx.x / p.nsl, sl = (int)blockIdx.x - grp * p.nsl;
+    const int blk0 = grp * T;
+    const int ub = sl * p.ups, ue = min(p.NU, ub + p.ups);  // the slice's units
+    const int NU = p.NU;
+    const int u0 = ub + wave * UPW;
 
     // x pieces: MFMA lane j + 16 kq multiplies row m = 16 mt + j at
     // k = u UK + 32 d + (int4: 8 kq; fp8: 16 (kq & 1) + 8 (kq >> 1)), so the
@@ -155,16 +171,17 @@ __global__ void __launch_bounds__(T == 1 ? 1024 : 512) gemv_panel(PanelParams p)
     }
     const int xsrc = quad_source(lane);
     auto xmove = [&](u32x4 v) -> u32x4 { return quad_to_mfma(v, xsrc); };
-    // the workgroup's blocks: tiles and (int4) scale quads; a block past the
-    // weight has empty ranges (zeros, no requests) and is never stored, and
-    // a unit past the row is past the ranges
+    // the workgroup's blocks: tiles and (int4) scale quads up to the end of
+    // the slice; a block past the weight has empty ranges (zeros, no
+    // requests) and is never stored, and a unit past the slice is past the
+    // ranges
     __amdgpu_buffer_rsrc_t wrs[T], srs[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         const bool live = blk0 + t < p.nblk;
         const uint8_t* chunk = p.w + (int64_t)(live ? blk0 + t : 0) * p.chunk;
-        wrs[t] = buffer_rsrc(chunk, live ? (uint32_t)NU * 1024u : 0u);
-        srs[t] = buffer_rsrc(chunk + (int64_t)NU * 1024, live && I4 ? (uint32_t)NU * 64u : 0u);
+        wrs[t] = buffer_rsrc(chunk, live ? (uint32_t)ue * 1024u : 0u);
+        srs[t] = buffer_rsrc(chunk + (int64_t)NU * 1024, live && I4 ? (uint32_t)ue * 64u : 0u);
     }
     const uint32_t wlane = j * 64 + kq * 16, slane = kq * 16;
 
@@ -175,7 +192,7 @@ __global__ void __launch_bounds__(T == 1 ? 1024 : 512) gemv_panel(PanelParams p)
         const int u = u0 + q;
         const uint32_t ux = (uint32_t)u * UK * 2;
         const __amdgpu_buffer_rsrc_t xrs =
-            buffer_rsrc(reinterpret_cast<const uint8_t*>(p.x) + ux, u < NU ? xbytes - ux : 0u);
+            buffer_rsrc(reinterpret_cast<const uint8_t*>(p.x) + ux, u < ue ? xbytes - ux : 0u);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -301,17 +318,14 @@ __global__ void __launch_bounds__(T == 1 ? 1024 : 512) gemv_panel(PanelParams p)
     __syncthreads();
 
     // each output (x row m, column c of the workgroup's 16 T): the sum over
-    // the waves in wave order, the fp8 row scale, the residual, the store
+    // the waves in wave order; then (one slice) the fp8 row scale, the
+    // residual and the store, or (several slices) the partial
     const int ncol = 16 * T;
     const int nout = M * ncol;
     const int wstride = T * MT * 256;
-    for (int o = tid; o < nout; o += nthr) {
-        const int m = o / ncol, c = o - m * ncol;
+    const int n_out = p.nblk * 16;
+    auto finish = [&](float a, int m, int c) {
         const int t = c >> 4, n = c & 15;
-        if (blk0 + t >= p.nblk) continue;
-        const float* rp = red + (t * MT + (m >> 4)) * 256 + (m & 15) * 16 + n;
-        float a = 0.0f;
-        for (int w = 0; w < NW; ++w) a += rp[w * wstride];
         if (!I4) {
             const float* rsc = reinterpret_cast<const float*>(p.w + (int64_t)(blk0 + t) * p.chunk + (int64_t)NU * 1024);
             a *= rsc[n];
@@ -327,15 +341,62 @@ __global__ void __launch_bounds__(T == 1 ? 1024 : 512) gemv_panel(PanelParams p)
             reinterpret_cast<float*>(p.out)[oi] = a;
         else
             reinterpret_cast<uint16_t*>(p.out)[oi] = f32_to_bf16(a);
+    };
+    for (int o = tid; o < nout; o += nthr) {
+        const int m = o / ncol, c = o - m * ncol;
+        const int t = c >> 4, n = c & 15;
+        if (blk0 + t >= p.nblk) continue;
+        const float* rp = red + (t * MT + (m >> 4)) * 256 + (m & 15) * 16 + n;
+        float a = 0.0f;
+        for (int w = 0; w < NW; ++w) a += rp[w * wstride];
+        if (p.nsl == 1)
+            finish(a, m, c);
+        else  // consecutive outputs of a row are consecutive columns: coalesced
+            __hip_atomic_store(p.part + ((int64_t)sl * M + m) * n_out + blk0 * 16 + c, a, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     }
+    if (p.nsl == 1) return;
+    int& last_arrival = *reinterpret_cast<int*>(smem + panel_lds(NW, T, MT) - 16);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(&p.cnt[grp], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_arrival = prev == (unsigned)p.nsl - 1u;
+    }
+    __syncthreads();
+    if (!last_arrival) return;
+    // the last arrival: each output's slices in slice order, kPanelSumBatch
+    // loads in flight per batch (slice indices clamped into range)
+    constexpr int kPanelSumBatch = 8;
+    const int64_t sstride = (int64_t)M * n_out;
+    for (int o = tid; o < nout; o += nthr) {
+        const int m = o / ncol, c = o - m * ncol;
+        if (blk0 + (c >> 4) >= p.nblk) continue;
+        const float* pp = p.part + (int64_t)m * n_out + blk0 * 16 + c;
+        float a = 0.0f;
+        for (int s0 = 0; s0 < p.nsl; s0 += kPanelSumBatch) {
+            float v[kPanelSumBatch];
+#pragma unroll
+            for (int u = 0; u < kPanelSumBatch; ++u)
+                v[u] = __hip_atomic_load(pp + min(s0 + u, p.nsl - 1) * sstride, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int u = 0; u < kPanelSumBatch; ++u)
+                if (s0 + u < p.nsl) a += v[u];
+        }
+        finish(a, m, c);
+    }
+    if (tid == 0) __hip_atomic_store(&p.cnt[grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- host side -----------------------------------------------------------------
 
 struct PanelLaunch {
     int nw, upw, mt, T;
-    unsigned grid;
+    int nsl, ups;    // K slices and units per slice
+    unsigned grid;   // row-block groups x nsl
     size_t lds;
+    size_t ws;       // workspace bytes (nsl > 1)
 };
 
 template <int WF, int MT, int T, int UPW>

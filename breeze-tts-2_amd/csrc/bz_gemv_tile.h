@@ -25,14 +25,19 @@
 //     in LDS as [unit][row] so the 4 rows of a lane come in one 16-byte read;
 //   * one slice: the epilogue (fp8 row scale, residual) is applied straight
 //     from the accumulators.  Several slices: fp32 partials go to the
-//     workspace with agent-scope stores (they reach the point of coherence
-//     without an L2 write-back), each workgroup waits for its stores, counts
-//     its arrival on the column block's counter, and the last one sums the
-//     slices in slice order (the result does not depend on arrival order),
-//     applies the epilogue and resets the counter to zero for the next call.
+//     workspace with 16-byte agent-scope stores (they reach the point of
+//     coherence without an L2 write-back), each workgroup waits for its
+//     stores, counts its arrival on the column block's counter, and the last
+//     one sums the slices in slice order (the result does not depend on
+//     arrival order) with all its 16-byte loads of a batch of slices in
+//     flight, applies the epilogue and resets the counter to zero for the
+//     next call.  (Measured on MI355X, int4 K10240 N2560 M = 32: 4-byte
+//     partial stores and loads in batches of 8 outputs x 4 slices made the
+//     last arrival's sum a tail of several memory round trips.)
 //
 // Workspace: kTileCounters uint32 counters (zero before the first call; every
-// call leaves them zero), then fp32 partials [nsl][M][N_out].
+// call leaves them zero), then fp32 partials [nsl][N_out][MP], MP = M rounded
+// up to a multiple of 4 (tile_part_rows).
 #pragma once
 #include "bz_gemv_mfma.h"
 
@@ -131,48 +136,65 @@ __device__ __forceinline__ void tile_store(const TileParams& tp, float v, int r,
         reinterpret_cast<uint16_t*>(p.out)[oi] = f32_to_bf16(v);
 }
 
+// Partials of one slice, column-major: the MP = M rounded up to 4 rows of
+// column c at [c * MP, c * MP + MP), so the four consecutive rows an MFMA lane
+// holds (rows 4 kb .. 4 kb + 3 of column j) are one 16-byte store and the last
+// arrival reads them back as one 16-byte load per slice.  Rows M..MP-1 hold
+// sums of clamped x rows and are never stored as outputs.
+__host__ __device__ inline int tile_part_rows(int M) { return (M + 3) & ~3; }
+
 // The last arrival's sum of a column block's partials over the slices, in
-// slice order, and the epilogue: each thread sums RQ outputs per pass, RS
-// slices of each in flight per batch (indices clamped into range, so the
-// loads stay straight-line).
-template <int WF, int RQ, int RS>
-__device__ __forceinline__ void tile_sum_slices(const TileParams& tp, int cb, int CBW, int nout, int64_t sstride,
-                                                int tid, int nthr) {
+// slice order, and the epilogue: each thread takes G groups of four rows of
+// one column per pass and has G x RS 16-byte loads of partials in flight per
+// batch of RS slices (slice and group indices clamped into range, so the
+// loads stay straight-line).  Loads and stores of partials carry the
+// agent-scope cache policy (sc1): they reach the point of coherence, not a
+// non-coherent L2 line of another XCD.
+template <int WF, int G, int RS>
+__device__ __forceinline__ void tile_sum_slices(const TileParams& tp, int cb, int CBW, int64_t sstride, int tid,
+                                                int nthr) {
     const GemvParams& p = tp.p;
-    const int nsl = tp.nsl;
-    const int cbw_log2 = __builtin_ctz(CBW);
-    for (int i0 = 0; i0 < nout; i0 += RQ * nthr) {
-        float sum[RQ];
-        int off[RQ];
+    const int nsl = tp.nsl, M = tp.M, MP = tile_part_rows(M);
+    const int rq = MP >> 2;             // groups of four rows per column
+    const int ngrp = CBW * rq;          // groups of the column block
+    const int c0 = cb * CBW;
+    for (int i0 = 0; i0 < ngrp; i0 += G * nthr) {
+        f32x4_t sum[G];
+        uint32_t off[G];
 #pragma unroll
-        for (int q = 0; q < RQ; ++q) {
-            sum[q] = 0.0f;
-            const int i = min(i0 + tid + q * nthr, nout - 1);
-            const int r = i >> cbw_log2;
-            off[q] = r * p.n_out + min(cb * CBW + (i - r * CBW), p.n_out - 1);
+        for (int q = 0; q < G; ++q) {
+            sum[q] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            const int i = min(i0 + tid + q * nthr, ngrp - 1);
+            const int cl = i / rq, g = i - cl * rq;
+            off[q] = (uint32_t)((min(c0 + cl, p.n_out - 1) * MP + 4 * g) * 4);
         }
         for (int s0 = 0; s0 < nsl; s0 += RS) {
-            float v[RQ][RS];
+            u32x4 v[G][RS];
 #pragma unroll
             for (int u = 0; u < RS; ++u) {
-                const float* ps = tp.part + min(s0 + u, nsl - 1) * sstride;  // uniform
+                const __amdgpu_buffer_rsrc_t r =
+                    buffer_rsrc(tp.part + min(s0 + u, nsl - 1) * sstride, (uint32_t)(sstride * 4));  // uniform
 #pragma unroll
-                for (int q = 0; q < RQ; ++q)
-                    v[q][u] = __hip_atomic_load(ps + off[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int q = 0; q < G; ++q) v[q][u] = __builtin_amdgcn_raw_buffer_load_b128(r, off[q], 0, kCpolAgent);
             }
 #pragma unroll
-            for (int q = 0; q < RQ; ++q)
+            for (int q = 0; q < G; ++q)
 #pragma unroll
                 for (int u = 0; u < RS; ++u)
-                    if (s0 + u < nsl) sum[q] += v[q][u];
+                    if (s0 + u < nsl)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) sum[q][e] += __uint_as_float(v[q][u][e]);
         }
 #pragma unroll
-        for (int q = 0; q < RQ; ++q) {
+        for (int q = 0; q < G; ++q) {
             const int i = i0 + tid + q * nthr;
-            if (i >= nout) continue;
-            const int r = i >> cbw_log2;
-            const int c = cb * CBW + (i - r * CBW);
-            if (c < p.n_out) tile_store<WF>(tp, sum[q], r, c);
+            if (i >= ngrp) continue;
+            const int cl = i / rq, g = i - cl * rq;
+            const int c = c0 + cl;
+            if (c >= p.n_out) continue;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (4 * g + e < M) tile_store<WF>(tp, sum[q][e], 4 * g + e, c);
         }
     }
 }
@@ -395,24 +417,24 @@ __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
         return;
     }
 
-    // 4b. several slices: partials, arrival, and the last arrival's sum.
-    //    Partial offsets inside a slice are 32-bit (M * N_out < 2^31).
-    const int64_t sstride = (int64_t)M * p.n_out;
+    // 4b. several slices: partials (column-major, 16-byte agent-scope
+    //    stores), arrival, and the last arrival's sum.  Partial offsets inside
+    //    a slice are 32-bit (host: MP * N_out * 4 < 2^31).
+    const int MP = tile_part_rows(M);
+    const int64_t sstride = (int64_t)MP * p.n_out;
     if (active) {
-        float* ps = tp.part + sl * sstride;  // uniform
+        const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(tp.part + sl * sstride, (uint32_t)(sstride * 4));  // uniform
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int c = col0 + 16 * t + j;
             if (c >= p.n_out) continue;
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int r = 16 * mb + 4 * kb + q;
-                    if (r < M)
-                        __hip_atomic_store(ps + (r * p.n_out + c), acc[t][mb][q], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                }
+            for (int mb = 0; mb < MB; ++mb) {
+                const int r0 = 16 * mb + 4 * kb;
+                if (r0 < M)
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[t][mb]), prs,
+                                                           (uint32_t)((c * MP + r0) * 4), 0, kCpolAgent);
+            }
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -423,18 +445,11 @@ __global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
     }
     __syncthreads();
     if (!last_arrival) return;
-    // The sum over slices, in slice order.  Threads with 8 or more outputs
-    // (M = 32 of a 128-column block over 512 threads) take 8 outputs x 4
-    // slices of loads per batch, which halves the memory round trips of
-    // 4 x 4; fewer outputs keep 4 x 4.  Wider batches measured slower at
-    // M = 32 (8 x 8 over 10 slices: 0.8 us with clamped loads, 1.8 us with
-    // range-checked buffer loads).
-    const int CBW = NW * 16 * T;  // columns of a block (a power of two)
-    const int nout = M * CBW;
-    if (nout >= 8 * nthr)
-        tile_sum_slices<WF, 8, 4>(tp, cb, CBW, nout, sstride, tid, nthr);
-    else
-        tile_sum_slices<WF, 4, 4>(tp, cb, CBW, nout, sstride, tid, nthr);
+    // The sum over slices, in slice order: two groups of four outputs per
+    // thread and eight slices of each in flight per batch (M = 32 of a
+    // 128-column block over 512 threads: one pass, batches of 16 loads).
+    const int CBW = NW * 16 * T;  // columns of a block
+    tile_sum_slices<WF, 2, 8>(tp, cb, CBW, sstride, tid, nthr);
     if (tid == 0) __hip_atomic_store(&tp.cnt[cb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

@@ -210,8 +210,8 @@ def test_gemv_null_descriptor(L):
 
 def test_workspace_sizes(L):
     """0 below 5 rows, with an RMSNorm or a SiLU gate, or for an invalid
-    descriptor; otherwise the counters (16 KB) plus nsl x M x N fp32
-    partials of the several-row tile path."""
+    descriptor; otherwise the counters (16 KB) plus nsl x N x MP fp32
+    partials of the several-row tile path (MP = M rounded up to 4)."""
     ws = lambda **kw: L.lib().bz_gemv_workspace(ctypes.byref(_desc(L, **kw)))  # noqa: E731
     assert ws() == 0
     assert ws(M=4) == 0
@@ -223,7 +223,8 @@ def test_workspace_sizes(L):
     assert ws(M=8, N=128, epilogue=1) == 0
     assert ws(M=8, abi_version=99) == 0
     assert ws(M=2, cfg_path=4, cfg_slices=1) == 0              # one slice: no partials
-    assert ws(M=2, cfg_path=4, cfg_slices=2) == 16384 + 2 * 2 * 64 * 4
+    assert ws(M=2, cfg_path=4, cfg_slices=2) == 16384 + 2 * 4 * 64 * 4   # rows padded to 4
+    assert ws(M=6, cfg_path=4, cfg_slices=2) == 16384 + 2 * 8 * 64 * 4
 
 
 @pytest.mark.parametrize(

@@ -1,7 +1,7 @@
 """GPU parity of the several-row panel kernel (GEMV path 6: up to 32 rows of x
 against an unpaired tiled int4 / fp8 weight, every workgroup covering the
-whole K of its row blocks, x read straight into the matrix-core operands)
-through the C ABI, against the CPU oracle.
+whole K of its row blocks or one of several K slices, x read straight into
+the matrix-core operands) through the C ABI, against the CPU oracle.
 
 Bars as for the other GEMV paths:
   * max|out-ref|/max|ref| <= 4e-3 against the float64 dequantize-then-matmul
@@ -159,9 +159,8 @@ def test_panel_full_size(fmt, n, k, m):
 
 def test_panel_automatic_choice():
     """The built-in rule takes the panel kernel (bit-identical to forcing it)
-    from 5 rows on while M K <= 196608, for fp8 at 3-4 rows over >= 1280 row
-    blocks, and not beyond (there the tile kernel runs; same result within
-    the bar)."""
+    from 5 rows on, and for fp8 at 3-4 rows over >= 1280 row blocks; not for
+    int4 at 3 rows (another path: same result within the bar)."""
     from breeze_amd import tuning
 
     saved = dict(tuning._TABLES)
@@ -169,8 +168,8 @@ def test_panel_automatic_choice():
     tuning._TABLES[tuning.arch_of(torch.device("cuda"))] = {}  # the built-in rule, not the table
     try:
         for fmt, n, k, m, panel in [("int4", 2560, 10240, 16, True), ("int4", 2560, 4096, 32, True),
-                                    ("fp8", 20480, 2560, 3, True), ("int4", 2560, 10240, 32, False),
-                                    ("int4", 20480, 2560, 3, False)]:
+                                    ("fp8", 20480, 2560, 3, True), ("int4", 2560, 10240, 32, True),
+                                    ("fp8", 2560, 10240, 32, True), ("int4", 20480, 2560, 3, False)]:
             buf, wf, w_eff = _weight(fmt, n, k, 600 + m)
             x = _x(m, k, 601)
             auto = _run(buf, wf, n, x, cfg=(0, 0, 0, 0))
@@ -249,7 +248,8 @@ def test_panel_rejects_what_it_cannot_run():
 def test_panel_taken_without_a_workspace():
     """Through the C ABI with no workspace, several rows that the rule gives
     the tile kernel (K10240 at M = 32, which needs split-K partials) run on
-    the panel kernel instead: bit-identical to forcing path 6."""
+    the panel kernel over the whole K instead: bit-identical to forcing path
+    6 with one slice."""
     import ctypes
 
     from breeze_amd import _lib
@@ -267,6 +267,111 @@ def test_panel_taken_without_a_workspace():
     d.out, d.ldo = out.data_ptr(), out.stride(0)
     assert _lib.lib().bz_gemv_workspace(ctypes.byref(d)) > 0  # the rule's tile kernel would need one
     _lib.check(_lib.lib().bz_gemv(ctypes.byref(d), _lib.stream_of(x)), "bz_gemv")
-    want = G.gemv(x, buf, wf, n, cfg=(0, 0, 0, PANEL))
+    want = G.gemv(x, buf, wf, n, cfg=(0, 0, 0, PANEL, 1))
     assert torch.equal(out, want)
     assert O.rel_err(f32(out), _ref(_x(m, k, 1001), w_eff)) <= TIGHT
+
+
+# ---------------------------------------------------------------------------
+# K slices: fp32 sums per slice in the workspace, the last arrival of each
+# row-block group adds them in slice order and applies the epilogue
+# ---------------------------------------------------------------------------
+
+SLICED = [
+    # (fmt, n, k, m, blocks, slices)
+    ("int4", 112, 1280, 9, 2, 3),      # 10 units / 3 slices: 4, 4, 2; a partial last group
+    ("int4", 1024, 4096, 32, 3, 5),    # 32 units / 5: 7 x 4 + 4
+    ("int4", 2560, 10240, 17, 1, 2),   # 16 waves x 3 units per slice
+    ("fp8", 112, 1280, 9, 2, 3),       # 20 units / 3
+    ("fp8", 1024, 4096, 32, 3, 4),
+    ("fp8", 2560, 10240, 16, 5, 8),
+]
+
+
+@pytest.mark.parametrize("fmt,n,k,m,blocks,slices", SLICED, ids=[f"{c[0]}-N{c[1]}-K{c[2]}-M{c[3]}-T{c[4]}-S{c[5]}"
+                                                                  for c in SLICED])
+def test_panel_slices_match_oracle_and_whole_k(fmt, n, k, m, blocks, slices):
+    buf, wf, w_eff = _weight(fmt, n, k, 1100 + slices, symmetric=(m % 2 == 1))
+    x = _x(m, k, 1101 + m)
+    res = _x(m, n, 1102) if slices % 2 else None
+    out_dtype = torch.float32 if m == 17 else torch.bfloat16
+    got = _run(buf, wf, n, x, cfg=(0, 0, blocks, PANEL, slices), res_bits=res, out_dtype=out_dtype)
+    assert O.rel_err(f32(got), _ref(x, w_eff, res)) <= TIGHT
+    # the same sums in another order (slice by slice): within one bf16 step
+    # of the whole-K launch (one block per workgroup: up to 16 waves, enough
+    # for every K here)
+    whole = _run(buf, wf, n, x, cfg=(0, 0, 1, PANEL, 1), res_bits=res, out_dtype=out_dtype)
+    assert O.rel_err(f32(got), f32(whole)) <= 2 ** -7
+    # every call leaves the arrival counters zero: a second and third call are
+    # bit-identical (a counter left non-zero would pick the wrong last arrival)
+    for _ in range(2):
+        assert torch.equal(_run(buf, wf, n, x, cfg=(0, 0, blocks, PANEL, slices), res_bits=res,
+                                out_dtype=out_dtype), got)
+
+
+def test_panel_rule_slices_at_full_size():
+    """K10240 N2560 at M = 32: the rule's slices (int4 2 blocks x 3 slices,
+    fp8 3 x 4) are what the automatic call runs, bit for bit."""
+    for fmt, blocks, slices in (("int4", 2, 3), ("fp8", 3, 4)):
+        buf, wf, w_eff = _weight(fmt, 2560, 10240, 1200)
+        x = _x(32, 10240, 1201)
+        auto = _run(buf, wf, 2560, x, cfg=(0, 0, 0, 0))
+        forced = _run(buf, wf, 2560, x, cfg=(0, 0, blocks, PANEL, slices))
+        assert torch.equal(auto, forced), fmt
+        assert O.rel_err(f32(auto), _ref(x, w_eff)) <= TIGHT
+
+
+def test_panel_slices_graph_replays_match_eager():
+    n, k, m = 2560, 10240, 32
+    buf, wf, _ = _weight("fp8", n, k, 1300)
+    x = bf16_tensor(_x(m, k, 1301))
+    out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    call = lambda: G.gemv(x, buf, wf, n, out=out, cfg=(0, 0, 3, PANEL, 4))  # noqa: E731
+    call()
+    torch.cuda.synchronize()
+    want = out.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side), torch.cuda.graph(g, stream=side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    for i in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), i
+        _ = (x.float() * 2).sum().item()
+
+
+def test_panel_forced_slices_need_the_workspace():
+    """Through the C ABI: forced slices without a workspace are refused
+    (status 1) and nothing runs; the workspace the library asks for makes the
+    same call run."""
+    import ctypes
+
+    from breeze_amd import _lib
+
+    n, k, m = 256, 2048, 8
+    buf, wf, w_eff = _weight("int4", n, k, 1400)
+    xb = _x(m, k, 1401)
+    x = bf16_tensor(xb)
+    out = torch.zeros(m, n, device="cuda", dtype=torch.bfloat16)
+    d = _lib.GemvDesc()
+    d.abi_version = _lib.ABI_VERSION
+    d.M, d.N, d.K, d.group, d.wfmt = m, n, k, 128, wf
+    d.epilogue, d.out_dtype, d.residual_dtype = G.EPI_NONE, _lib.DT_BF16, _lib.DT_BF16
+    d.eps = 1e-6
+    d.x, d.ldx, d.w = x.data_ptr(), x.stride(0), buf.data_ptr()
+    d.out, d.ldo = out.data_ptr(), out.stride(0)
+    d.cfg_path, d.cfg_tiles, d.cfg_slices = PANEL, 2, 4
+    need = _lib.lib().bz_gemv_workspace(ctypes.byref(d))
+    assert need == 16384 + 4 * m * n * 4
+    assert _lib.lib().bz_gemv(ctypes.byref(d), _lib.stream_of(x)) == _lib.ERR_INVALID_ARG
+    torch.cuda.synchronize()
+    assert not out.any()
+    ws = torch.zeros(need // 4, device="cuda", dtype=torch.int32)
+    d.workspace, d.workspace_bytes = ws.data_ptr(), need
+    _lib.check(_lib.lib().bz_gemv(ctypes.byref(d), _lib.stream_of(x)), "bz_gemv")
+    assert O.rel_err(f32(out), _ref(xb, w_eff)) <= TIGHT
+    assert not ws[:4096].any()  # the counters are left zero
