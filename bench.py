@@ -110,7 +110,11 @@ PROFILE_CASES = [
     ("fp8 down K10240 N2560 M1", "fp8", "tiled", 2560, 10240, 1, 0, False),
     ("int4 qkv K2560 N6144 M1", "int4", "tiled", 6144, 2560, 1, 0, True),
     ("int4 o_proj K4096 N2560 M1", "int4", "tiled", 2560, 4096, 1, 2, False),
+    ("fp8 qkv K2560 N4096 M1", "fp8", "tiled", 4096, 2560, 1, 0, True),
+    ("fp8 o_proj K4096 N2560 M1", "fp8", "tiled", 2560, 4096, 1, 2, False),
     ("int4 C4 K10240 N2560 M32 (row-major, split-K tile)", "int4", "rowmajor", 2560, 10240, 32, 0, False),
+    ("int4 C4 K10240 N2560 M32 (tiled, panel, 3 K slices)", "int4", "tiled", 2560, 10240, 32, 0, False),
+    ("fp8 C4 K10240 N2560 M32 (tiled, panel, 4 K slices)", "fp8", "tiled", 2560, 10240, 32, 0, False),
     ("int4 C4 K2560 N20480 M32 (tiled, panel)", "int4", "tiled", 20480, 2560, 32, 0, False),
     ("fp8 C4 K2560 N20480 M32 (tiled, panel)", "fp8", "tiled", 20480, 2560, 32, 0, False),
 ]
@@ -330,7 +334,8 @@ def main() -> int:
     traffic = read_traffic()
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                "kernel": "gemv_stream int4 tiled-paired SiLU-gate K2560 N20480 M1 (+RMSNorm)",
+                "kernel": "gemv_wide int4 tiled-paired SiLU-gate K2560 N20480 M1 (+RMSNorm), 5 row blocks "
+                          "per workgroup",
                 "algorithmic_bytes": b_gu, "avg_launch_us": round(us_gu, 3)}
     log(f"gate|up {us_gu:.2f} us ({achieved:.0f} GB/s), down {us_dn:.2f} us "
         f"({b_dn / us_dn / 1e3:.0f} GB/s)")
@@ -608,7 +613,7 @@ def pmc_summary(fetch_dir: str, write_dir: str) -> int:
     print(f"HBM traffic per launch, median of {PROFILE_REPS} launches per case; counters scaled by a "
           f"{COPY_BYTES}-byte copy: FETCH_SIZE {f_copy:.1f} KiB -> read scale {fr:.4f}, "
           f"WRITE_SIZE {w_copy:.1f} KiB -> write scale {wr:.4f}")
-    print(f"{'case':52s} {'algorithmic B':>13s} {'fetch B':>11s} {'write B':>9s} {'traffic B':>11s} "
+    print(f"{'case':56s} {'algorithmic B':>13s} {'fetch B':>11s} {'write B':>9s} {'traffic B':>11s} "
           f"{'traffic/algo':>12s}  kernel")
     lines = []
     for case, (kname, f), (_, w) in zip(PROFILE_CASES, fetch, write):
@@ -616,7 +621,7 @@ def pmc_summary(fetch_dir: str, write_dir: str) -> int:
         algo = algo_bytes(4 if fmt == "int4" else 8, N, K, M, norm, epi)
         fb, wb = int(round(f * fr * 1024)), int(round(w * wr * 1024))
         kern = re.search(r"gemv_\w+<[^>]*>", kname)
-        print(f"{name:52s} {algo:13d} {fb:11d} {wb:9d} {fb + wb:11d} {(fb + wb) / algo:12.4f}  "
+        print(f"{name:56s} {algo:13d} {fb:11d} {wb:9d} {fb + wb:11d} {(fb + wb) / algo:12.4f}  "
               f"{kern.group(0) if kern else kname[:60]}")
         lines.append(f"traffic_bytes_per_launch[{name}]: {fb + wb}")
     for line in lines:
