@@ -129,7 +129,7 @@ typedef enum bz_dtype {
  * waves per workgroup (0 = the kernel's rule), cfg_depth unused; 6 = the
  * several-row panel kernel of the tiled formats, see below).  Without a cfg
  * the rule takes the several-block kernel for weights of more than 256 row
- * blocks (one workgroup per CU) and for fp8 rows of 80 units or more.
+ * blocks (one workgroup per CU) and for fp8 rows of 64 units or more.
  * Used by tuning sweeps.
  *
  * Several rows (path 4).  Up to 32 rows of x per launch stream every weight
@@ -150,13 +150,17 @@ typedef enum bz_dtype {
  * rows of x per launch against an unpaired tiled int4 or fp8 weight
  * (BZ_W_INT4_TILED, BZ_W_FP8_TILED), no RMSNorm, epilogue NONE or RESIDUAL,
  * no second store: each workgroup of cfg_waves waves (0: about 5 units per
- * wave; at most 16, or 8 with several blocks) covers the whole K of
- * cfg_tiles consecutive 16-row blocks (1..5; 0: enough to keep about 256
- * workgroups), so it needs no workspace; larger M runs 32 rows per launch.
- * The automatic rule takes it for these weights from M = 5 on while
- * min(M, 32) * K <= 196608 (beyond that the tile kernel, or the panel
- * kernel when `workspace` is too small for the tile kernel), and for fp8 at
- * M = 3-4 with N >= 20480; the streaming kernel otherwise.
+ * wave; at most 16, or 8 with several blocks) covers cfg_tiles consecutive
+ * 16-row blocks (1..5; 0: enough to keep about 256 workgroups, or 2 (int4)
+ * / 3 (fp8) with K slices) over the whole K or over one of cfg_slices K
+ * slices (0: one while the x of a launch is at most 256 KB, else about 240
+ * workgroups in all); larger M runs 32 rows per launch.  With more than
+ * one slice the slices' fp32 sums go to `workspace` as for path 4
+ * (bz_gemv_workspace bytes); forced slices without it return
+ * BZ_ERR_INVALID_ARG, and the rule's slices without it fall back to the
+ * whole K.  The automatic rule takes this path for these weights from M = 5
+ * on, and for fp8 at M = 3-4 with N >= 20480; the streaming kernels
+ * otherwise.
  */
 typedef struct bz_gemv_desc {
     int32_t abi_version;      /* must be BZ_ABI_VERSION */
@@ -167,7 +171,7 @@ typedef struct bz_gemv_desc {
     int32_t out_dtype;        /* bz_dtype */
     int32_t residual_dtype;   /* bz_dtype */
     int32_t cfg_depth, cfg_waves, cfg_tiles, cfg_path;  /* 0 = automatic */
-    int32_t cfg_slices;       /* path 4: K slices (0 = automatic) */
+    int32_t cfg_slices;       /* paths 4 and 6: K slices (0 = automatic) */
     float eps;
     const void* x;  int64_t ldx;
     const void* w;
@@ -200,10 +204,11 @@ const char* bz_strerror(int status);
  * models/fused/kernels.py:179,192-198, is shared by every stream). */
 int bz_stream_capture(void* stream, int32_t* active, uint64_t* id);
 
-/* Workspace bytes the several-row tile path (path 4) needs for this
- * descriptor: 0 when bz_gemv would not take that path (M < 5 without
- * cfg_path 4, an RMSNorm or SiLU-gate call, unsupported K or group) or runs
- * it with a single K slice.  Returns 0 for an invalid descriptor. */
+/* Workspace bytes the several-row kernels (the tile path 4, the panel path
+ * 6) need for this descriptor: 0 when bz_gemv would take neither (M < 5
+ * without cfg_path 4 or 6, an RMSNorm or SiLU-gate call, unsupported K or
+ * group) or runs it with a single K slice.  Returns 0 for an invalid
+ * descriptor. */
 size_t bz_gemv_workspace(const bz_gemv_desc* d);
 
 /* The fused decode GEMV.  Replaces, as one launch:
