@@ -172,6 +172,12 @@ def main() -> int:
                     help="only launch the PROFILE_CASES GEMVs (eagerly) and a 256 MiB copy, for counter runs")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarize two rocprofv3 --pmc runs of --profile-gemvs")
+    ap.add_argument("--config-summary", metavar="DETAIL_FILE",
+                    help="print the C1-C4 configuration table, the floors, the decode steps and the library "
+                         "comparator from a --detail-out file")
+    ap.add_argument("--sq-summary", metavar="PMC_DIR",
+                    help="per-tile instruction and wait counters of the PROFILE_CASES GEMVs from a rocprofv3 "
+                         "--pmc run (SQ_ counters) of --profile-gemvs")
     ap.add_argument("--profile-tiles", action="store_true",
                     help="only launch the several-row (C4, M = 16 and 32) GEMVs eagerly, for counter runs")
     ap.add_argument("--profile-depth", action="store_true",
@@ -189,6 +195,10 @@ def main() -> int:
         return pmc_summary(*args.pmc_summary)
     if args.mfma_summary:
         return mfma_summary(*args.mfma_summary)
+    if args.sq_summary:
+        return sq_summary(args.sq_summary)
+    if args.config_summary:
+        return config_summary(args.config_summary)
     if args.step_summary:
         return step_summary(args.step_summary)
     if args.gpus != 1:
@@ -626,6 +636,89 @@ def pmc_summary(fetch_dir: str, write_dir: str) -> int:
         lines.append(f"traffic_bytes_per_launch[{name}]: {fb + wb}")
     for line in lines:
         print(line)
+    return 0
+
+
+def config_summary(path: str) -> int:
+    """The configuration table and its context (floors, decode steps, torch's
+    bf16 linear) from the full record bench.py wrote with --detail-out."""
+    rec = json.loads(open(path).read().strip().splitlines()[-1])
+    det = rec["detail"]
+    fl = det["floors"]
+    reads = ", ".join(f"{r['mib']} MiB {r['us']} us ({r['gbps']} GB/s)" for r in fl["read"])
+    line = (f"floors: empty graph node {fl['empty_node_us']} us; read-only kernel {reads}; fit "
+            f"{fl['read_fit']['fixed_us']} us + bytes at {fl['read_fit']['gbps']} GB/s")
+    cp = fl.get("copy_1gib") or {}
+    if cp:
+        line += f"; 1 GiB device copy {cp.get('us')} us ({cp.get('gbps_read_plus_write')} GB/s read+write)"
+    print(line)
+    for c in fl.get("chunks", []):
+        print(f"  read with a GEMV's decomposition: {c['what']}: {c['us']} us ({c['gbps']} GB/s)")
+    for c in fl.get("shared_x", []):
+        print(f"  whole-K read, x shared by all workgroups (bz_shared_read): {c['what']}, {c['workgroups']} x "
+              f"({c['x_bytes']} B of x + {c['w_bytes_per_workgroup']} B own): {c['us']} us "
+              f"({c['gbps_per_workgroup']} GB/s per workgroup)")
+    for key, what in (("decode_step", "tiled, M=1, copy for attention"), ("decode_step_m2", "tiled, M=2, copy for attention"),
+                      ("decode_step_rowmajor", "rowmajor, M=1, copy for attention"),
+                      ("decode_step_attn", "tiled, M=2, attention at 1023 of 1024")):
+        st = det.get(key)
+        if st:
+            print(f"26-layer decode step ({what}): {st['us']} us, roofline {st['roofline_us']} us ({st['x_roofline']}x)")
+    print()
+    print(f"{'config':52s} {'layout':8s} {'M':>3s} {'us':>8s} {'GB/s':>8s} {'roof_us':>8s} {'frac':>6s} {'TFLOP/s':>8s}  launch")
+    for r in det["configs"]:
+        print(f"{r['config']:52s} {r['layout']:8s} {r['M']:3d} {r['us']:8.2f} {r['gbps']:8.1f} {r['roofline_us']:8.2f} "
+              f"{r['frac']:6.3f} {r['tflops']:8.2f}  {r['launch']}")
+    print()
+    print("torch bf16 linear (hipBLASLt), cold weight copies (the reference's library comparator, bench_gemv.py:36-42)")
+    print(f"{'shape':32s} {'M':>2s} {'us':>8s} {'GB/s':>8s} {'roof_us':>8s} {'frac':>6s}")
+    for r in det["library_bf16_linear"]:
+        print(f"{r['shape']:32s} {r['M']:2d} {r['us']:8.2f} {r['gbps']:8.1f} {r['roofline_us']:8.2f} {r['frac']:6.3f}")
+    return 0
+
+
+# The SQ counters of one --pmc pass for sq_summary (at most 8 SQ_ counters in
+# a pass on this part).
+SQ_COUNTERS = ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_WAVE_CYCLES",
+               "SQ_WAIT_INST_ANY", "SQ_BUSY_CYCLES")
+
+
+def sq_summary(pmc_dir: str) -> int:
+    """Per launch of each PROFILE_CASES GEMV (median of its PROFILE_REPS
+    launches, the warm-up dropped), from a rocprofv3 --pmc run of
+    --profile-gemvs with SQ_COUNTERS: wave instructions per 1 KiB weight tile
+    by kind (VALU, MFMA, SALU, LDS), the waves, and the share of the waves'
+    cycles spent waiting for an instruction's operands or memory
+    (SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES)."""
+    import csv
+    import glob
+    import statistics
+
+    paths = glob.glob(os.path.join(pmc_dir, "**", "*counter_collection.csv"), recursive=True)
+    if not paths:
+        raise SystemExit(f"no counter_collection.csv under {pmc_dir}")
+    per = {}
+    for row in csv.DictReader(open(paths[0])):
+        if "gemv_" not in row["Kernel_Name"]:
+            continue
+        d = per.setdefault(int(row["Dispatch_Id"]), {"kernel": row["Kernel_Name"]})
+        d[row["Counter_Name"]] = d.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+    seq = [per[k] for k in sorted(per)]
+    n = 1 + PROFILE_REPS
+    if len(seq) != n * len(PROFILE_CASES):
+        raise SystemExit(f"{len(seq)} GEMV dispatches, expected {n * len(PROFILE_CASES)}")
+    print(f"wave instructions per 1 KiB weight tile and wait share, median of {PROFILE_REPS} launches per case")
+    print(f"{'case':56s} {'tiles':>7s} {'VALU/t':>7s} {'MFMA/t':>7s} {'SALU/t':>7s} {'LDS/t':>6s} {'waves':>6s} "
+          f"{'wait':>6s}  kernel")
+    for i, (name, fmt, layout, N, K, M, epi, norm) in enumerate(PROFILE_CASES):
+        c = seq[i * n + 1:(i + 1) * n]
+        med = {k: statistics.median(x.get(k, 0.0) for x in c) for k in SQ_COUNTERS}
+        tiles = N * K // (2048 if fmt == "int4" else 1024)  # 1 KiB of weight bytes per tile
+        wait = med["SQ_WAIT_INST_ANY"] / med["SQ_WAVE_CYCLES"] if med["SQ_WAVE_CYCLES"] else 0.0
+        kern = re.search(r"gemv_\w+<[^>]*>", c[0]["kernel"])
+        print(f"{name:56s} {tiles:7d} {med['SQ_INSTS_VALU'] / tiles:7.1f} {med['SQ_INSTS_MFMA'] / tiles:7.1f} "
+              f"{med['SQ_INSTS_SALU'] / tiles:7.1f} {med['SQ_INSTS_LDS'] / tiles:6.1f} {med['SQ_WAVES']:6.0f} "
+              f"{100 * wait:5.1f}%  {kern.group(0) if kern else ''}")
     return 0
 
 
