@@ -32,7 +32,7 @@
 //     sums its outputs' partials over the waves in wave order.
 //   * K slices (nsl > 1): the grid is (row-block groups) x nsl, the slices of
 //     one group consecutive.  Each workgroup stores its fp32 sums to the
-//     workspace ([nsl][M][N] after kTileCounters counters, agent-scope
+//     workspace ([nsl][M][N] after kTileCounters counters, 16-byte agent-scope
 //     stores that reach the point of coherence), waits for its stores and
 //     counts its arrival on the group's counter; the last arrival sums the
 //     slices in slice order (independent of the arrival order), applies the
@@ -317,43 +317,77 @@ __global__ void __launch_bounds__(T == 1 ? 1024 : 512) gemv_panel(PanelParams p)
             *reinterpret_cast<f32x4_t*>(red + ((wave * T + t) * MT + mt) * 256 + j * 16 + 4 * kq) = acc[t][mt];
     __syncthreads();
 
-    // each output (x row m, column c of the workgroup's 16 T): the sum over
-    // the waves in wave order; then (one slice) the fp8 row scale, the
-    // residual and the store, or (several slices) the partial
-    const int ncol = 16 * T;
-    const int nout = M * ncol;
+    // each item, x row m and columns c..c+3 of the workgroup's 16 T: the sum
+    // over the waves in wave order (one 16-byte LDS read per wave, all issued
+    // before the first add: a wave slot the workgroup does not have is read
+    // at the last present wave and added as zero, which leaves every sum
+    // bit-identical to the plain loop over the present waves); then (one
+    // slice) the epilogue, or (several slices) the partial.  The epilogue's
+    // own inputs (residual, fp8 row scales) are loaded first, so their round
+    // trip overlaps the LDS sums or the partials' loads.
+    const int nq = 4 * T;  // 4-column groups of a row
+    const int nitem = M * nq;
     const int wstride = T * MT * 256;
     const int n_out = p.nblk * 16;
-    auto finish = [&](float a, int m, int c) {
+    struct EpIn {
+        float r[4];   // residual
+        f32x4_t sc;   // fp8 row scales
+    };
+    auto ep_load = [&](int m, int c) {
+        EpIn e;
         const int t = c >> 4, n = c & 15;
-        if (!I4) {
-            const float* rsc = reinterpret_cast<const float*>(p.w + (int64_t)(blk0 + t) * p.chunk + (int64_t)NU * 1024);
-            a *= rsc[n];
-        }
         const int col = blk0 * 16 + c;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) e.r[q] = 0.0f;
         if (p.epi == BZ_EPI_RESIDUAL) {
             const int64_t ri = (int64_t)m * p.ldr + col;
-            a += p.res_f32 ? reinterpret_cast<const float*>(p.res)[ri]
-                           : bf16_to_f32(reinterpret_cast<const uint16_t*>(p.res)[ri]);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                e.r[q] = p.res_f32 ? reinterpret_cast<const float*>(p.res)[ri + q]
+                                   : bf16_to_f32(reinterpret_cast<const uint16_t*>(p.res)[ri + q]);
         }
-        const int64_t oi = (int64_t)m * p.ldo + col;
-        if (p.out_f32)
-            reinterpret_cast<float*>(p.out)[oi] = a;
-        else
-            reinterpret_cast<uint16_t*>(p.out)[oi] = f32_to_bf16(a);
+        e.sc = f32x4_t{1.0f, 1.0f, 1.0f, 1.0f};
+        if (!I4)
+            e.sc = *reinterpret_cast<const f32x4_t*>(p.w + (int64_t)(blk0 + t) * p.chunk + (int64_t)NU * 1024 + n * 4);
+        return e;
     };
-    for (int o = tid; o < nout; o += nthr) {
-        const int m = o / ncol, c = o - m * ncol;
+    auto ep_store = [&](f32x4_t a, const EpIn& e, int m, int c) {
+        const int64_t oi = (int64_t)m * p.ldo + blk0 * 16 + c;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float v = a[q];
+            if (!I4) v *= e.sc[q];
+            if (p.epi == BZ_EPI_RESIDUAL) v += e.r[q];
+            if (p.out_f32)
+                reinterpret_cast<float*>(p.out)[oi + q] = v;
+            else
+                reinterpret_cast<uint16_t*>(p.out)[oi + q] = f32_to_bf16(v);
+        }
+    };
+    // the partials of all slices through one buffer resource (host: nsl M N
+    // fp32 < 2^31 bytes), 16-byte agent-scope accesses
+    const __amdgpu_buffer_rsrc_t prs =
+        buffer_rsrc(p.part, p.nsl > 1 ? (uint32_t)((int64_t)p.nsl * M * n_out * 4) : 0u);
+    for (int it = tid; it < nitem; it += nthr) {
+        const int m = it / nq, c = (it - m * nq) * 4;
         const int t = c >> 4, n = c & 15;
         if (blk0 + t >= p.nblk) continue;
+        EpIn e;
+        if (p.nsl == 1) e = ep_load(m, c);
         const float* rp = red + (t * MT + (m >> 4)) * 256 + (m & 15) * 16 + n;
-        float a = 0.0f;
-        for (int w = 0; w < NW; ++w) a += rp[w * wstride];
+        f32x4_t v[kPanelMaxWaves];
+#pragma unroll
+        for (int w = 0; w < kPanelMaxWaves; ++w) v[w] = *reinterpret_cast<const f32x4_t*>(rp + min(w, NW - 1) * wstride);
+        f32x4_t a = {0.0f, 0.0f, 0.0f, 0.0f};
+        const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int w = 0; w < kPanelMaxWaves; ++w) a += w < NW ? v[w] : zero;
         if (p.nsl == 1)
-            finish(a, m, c);
-        else  // consecutive outputs of a row are consecutive columns: coalesced
-            __hip_atomic_store(p.part + ((int64_t)sl * M + m) * n_out + blk0 * 16 + c, a, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+            ep_store(a, e, m, c);
+        else
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, a), prs,
+                                                   (uint32_t)((((int64_t)sl * M + m) * n_out + blk0 * 16 + c) * 4), 0,
+                                                   kCpolAgent);
     }
     if (p.nsl == 1) return;
     int& last_arrival = *reinterpret_cast<int*>(smem + panel_lds(NW, T, MT) - 16);
@@ -365,26 +399,27 @@ __global__ void __launch_bounds__(T == 1 ? 1024 : 512) gemv_panel(PanelParams p)
     }
     __syncthreads();
     if (!last_arrival) return;
-    // the last arrival: each output's slices in slice order, kPanelSumBatch
-    // loads in flight per batch (slice indices clamped into range)
+    // the last arrival: each item's slices in slice order, kPanelSumBatch
+    // 16-byte loads in flight per batch (slice indices clamped into range)
     constexpr int kPanelSumBatch = 8;
-    const int64_t sstride = (int64_t)M * n_out;
-    for (int o = tid; o < nout; o += nthr) {
-        const int m = o / ncol, c = o - m * ncol;
+    for (int it = tid; it < nitem; it += nthr) {
+        const int m = it / nq, c = (it - m * nq) * 4;
         if (blk0 + (c >> 4) >= p.nblk) continue;
-        const float* pp = p.part + (int64_t)m * n_out + blk0 * 16 + c;
-        float a = 0.0f;
+        const EpIn e = ep_load(m, c);
+        const uint32_t off0 = (uint32_t)(((int64_t)m * n_out + blk0 * 16 + c) * 4);
+        const uint32_t sstride = (uint32_t)((int64_t)M * n_out * 4);
+        f32x4_t a = {0.0f, 0.0f, 0.0f, 0.0f};
         for (int s0 = 0; s0 < p.nsl; s0 += kPanelSumBatch) {
-            float v[kPanelSumBatch];
+            u32x4 v[kPanelSumBatch];
 #pragma unroll
             for (int u = 0; u < kPanelSumBatch; ++u)
-                v[u] = __hip_atomic_load(pp + min(s0 + u, p.nsl - 1) * sstride, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
+                v[u] = __builtin_amdgcn_raw_buffer_load_b128(prs, off0 + (uint32_t)min(s0 + u, p.nsl - 1) * sstride, 0,
+                                                             kCpolAgent);
 #pragma unroll
             for (int u = 0; u < kPanelSumBatch; ++u)
-                if (s0 + u < p.nsl) a += v[u];
+                if (s0 + u < p.nsl) a += __builtin_bit_cast(f32x4_t, v[u]);
         }
-        finish(a, m, c);
+        ep_store(a, e, m, c);
     }
     if (tid == 0) __hip_atomic_store(&p.cnt[grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
