@@ -443,8 +443,8 @@ constexpr int kPanelTargetWorkgroups = 240;
 // most kPanelSliceX, else about kPanelTargetWorkgroups workgroups in all), T
 // row blocks per workgroup (cfg_tiles: 1 to 5; default by the number of
 // blocks, or kPanelSliceBlocks* with slices), NW waves (cfg_waves; default
-// about 5 units per wave, at most 16 waves, 8 with several blocks) splitting
-// the slice's units UPW each.  `slices` > 0 overrides both the cfg and the
+// about 5 units per wave, 4 over K slices; at most 16 waves, 8 with several
+// blocks) splitting the slice's units UPW each.  `slices` > 0 overrides both the cfg and the
 // rule (1: no workspace).
 static int panel_plan(const bz_gemv_desc* d, int rows, PanelLaunch& l, int slices = 0) {
     const int wf = d->wfmt;
@@ -473,7 +473,7 @@ static int panel_plan(const bz_gemv_desc* d, int rows, PanelLaunch& l, int slice
     const int maxw = T == 1 ? kPanelMaxWaves : 8;
     int nw = d->cfg_waves;
     if (nw < 0 || nw > maxw) return BZ_ERR_INVALID_ARG;
-    if (!nw) nw = std::min(maxw, (ups + 4) / 5);
+    if (!nw) nw = std::min(maxw, nsl > 1 ? (ups + 3) / 4 : (ups + 4) / 5);  // sliced: int4 M = 16 7 x 4 units 9.25 us, 6 x 5 9.78
     const int need = (ups + nw - 1) / nw;
     int upw = 0;
     for (int u : kPanelUpw)
