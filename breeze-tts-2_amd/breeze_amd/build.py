@@ -34,6 +34,9 @@ HIP_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # leading scalar kernel arguments arrive in SGPRs at wave launch (kernarg
+    # preloading; the streaming kernels pass their hot fields that way)
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     f"-I{INCLUDE_DIR}",
     f"-I{SRC_DIR}",
 ]

@@ -123,9 +123,25 @@ __device__ __forceinline__ u32x4 swap_halves(u32x4 w) {
     return u32x4{a02[0], a13[0], a02[1], a13[1]};
 }
 
+// The fields the first loads need come as leading scalar arguments, which
+// the hardware preloads into SGPRs at wave launch (kernarg preloading, as
+// for the streaming kernels in bz_gemv_stream.h); the host passes the same
+// values in the struct.
 template <int WF, int MT, int T, int UPW>
-__global__ void __launch_bounds__(T == 1 ? 1024 : 512) gemv_panel(PanelParams p) {
+__global__ void __launch_bounds__(T == 1 ? 1024 : 512) gemv_panel(const uint8_t* hw, const uint16_t* hx, int hchunk, int hldx,
+                                                                  int hM, int hK, int hNU, int hnblk, int hnsl, int hups,
+                                                                  PanelParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    p.w = hw;
+    p.x = hx;
+    p.chunk = hchunk;
+    p.ldx = hldx;
+    p.M = hM;
+    p.K = hK;
+    p.NU = hNU;
+    p.nblk = hnblk;
+    p.nsl = hnsl;
+    p.ups = hups;
     constexpr bool I4 = tiled_i4(WF);
     constexpr int D = panel_depth(I4, MT, T, UPW);
     constexpr int NX = I4 ? 4 : 2;     // x pieces (16 bytes) per unit and row half
@@ -438,7 +454,9 @@ template <int WF, int MT, int T, int UPW>
 int launch_panel_kernel(const PanelParams& p, const PanelLaunch& l, hipStream_t st) {
     auto kern = gemv_panel<WF, MT, T, UPW>;
     if (l.lds > 65536 && raise_lds_limit(reinterpret_cast<const void*>(kern)) != BZ_OK) return BZ_ERR_LAUNCH;
-    hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, p);
+    if (p.chunk > 0x7FFFFFFF || p.ldx > 0x7FFFFFFF) return BZ_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, p.w, p.x, (int)p.chunk, (int)p.ldx, p.M, p.K, p.NU,
+                       p.nblk, p.nsl, p.ups, p);
     return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }
 

@@ -63,8 +63,11 @@ __host__ __device__ constexpr int wide_max_upw(int wf, int mm) { return tiled_i4
 constexpr int kWideMaxBlocks = 8;
 
 template <int WF, int MM, int UPW>
-__global__ void __launch_bounds__(1024) gemv_wide(StreamParams p, int T, int nblk) {
+__global__ void __launch_bounds__(1024) gemv_wide(const uint8_t* hw, const uint16_t* hx, const uint16_t* hg, int hchunk,
+                                                  int hldx, int hK, int hNU, int hM, int hnorm, int T, int nblk,
+                                                  StreamParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    stream_hot(p, hw, hx, hg, hchunk, hldx, hK, hNU, hM, hnorm);  // the preloaded arguments (bz_gemv_stream.h)
     constexpr bool I4 = tiled_i4(WF);
     constexpr bool PAIR = tiled_paired(WF);
     constexpr int BPU = tiled_unit_k(WF) / 8;   // blocks of 8 x values per unit
@@ -359,7 +362,9 @@ template <int WF, int MM, int UPW>
 int launch_wide_kernel(const StreamParams& p, const WideLaunch& l, int nblk, hipStream_t st) {
     auto kern = gemv_wide<WF, MM, UPW>;
     if (l.lds > 65536 && raise_lds_limit(reinterpret_cast<const void*>(kern)) != BZ_OK) return BZ_ERR_LAUNCH;
-    hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, p, l.T, nblk);
+    if (!stream_hot_ok(p)) return BZ_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, p.w, p.x, p.gamma, (int)p.chunk, (int)p.ldx, p.K,
+                       p.NU, p.M, p.norm, l.T, nblk, p);
     return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }
 
