@@ -375,7 +375,23 @@ __device__ __forceinline__ float bcast(float v, int lane) {
 // DL = D / 64 columns per lane; GM = 4 or 16 heads of register state (G <=
 // GM); F32C: fp32 cache; FUSED: q (and the new k, v) computed from qkv.
 template <int DL, int GM, bool F32C, bool FUSED, int NWV>
-__global__ void __launch_bounds__(64 * NWV) attn_kernel(AttnParams a) {
+__global__ void __launch_bounds__(64 * NWV) attn_kernel(const void* hrows, const void* hcos, const void* hsin,
+                                                        const int64_t* hpos, void* hkc, void* hvc, int hld_qkv, int hG,
+                                                        AttnParams a) {
+    // the fields of the first loads, preloaded into SGPRs at wave launch
+    // (kernarg preloading, as for the GEMV kernels); the host passes the same
+    // values in the struct
+    if constexpr (FUSED)
+        a.qkv = static_cast<const uint16_t*>(hrows);
+    else
+        a.q = static_cast<const float*>(hrows);
+    a.cosp = hcos;
+    a.sinp = hsin;
+    a.pos = hpos;
+    a.kc = hkc;
+    a.vc = hvc;
+    a.ld_qkv = hld_qkv;
+    a.G = hG;
     constexpr int kAttnWaves = NWV;
     constexpr int kAttnThreads = 64 * NWV;
     constexpr int D = 64 * DL;
@@ -799,12 +815,17 @@ __global__ void __launch_bounds__(64 * NWV) attn_kernel(AttnParams a) {
 // blocks in turn per wave on the double-buffered path, or the VALU path).
 template <int DL, int GM, bool FUSED>
 static void launch_attn(const AttnParams& a, bool f32c, dim3 grid, hipStream_t st) {
+    const void* rows = FUSED ? static_cast<const void*>(a.qkv) : static_cast<const void*>(a.q);
+    const int ld = (int)a.ld_qkv;  // bz_attn_step: checked to fit 32 bits
     if (f32c)
-        hipLaunchKernelGGL((attn_kernel<DL, GM, true, FUSED, 4>), grid, dim3(64 * 4), 0, st, a);
+        hipLaunchKernelGGL((attn_kernel<DL, GM, true, FUSED, 4>), grid, dim3(64 * 4), 0, st, rows, a.cosp, a.sinp, a.pos,
+                           a.kc, a.vc, ld, a.G, a);
     else if constexpr (DL <= 4 && GM == 4)
-        hipLaunchKernelGGL((attn_kernel<DL, GM, false, FUSED, 8>), grid, dim3(64 * 8), 0, st, a);
+        hipLaunchKernelGGL((attn_kernel<DL, GM, false, FUSED, 8>), grid, dim3(64 * 8), 0, st, rows, a.cosp, a.sinp, a.pos,
+                           a.kc, a.vc, ld, a.G, a);
     else
-        hipLaunchKernelGGL((attn_kernel<DL, GM, false, FUSED, 4>), grid, dim3(64 * 4), 0, st, a);
+        hipLaunchKernelGGL((attn_kernel<DL, GM, false, FUSED, 4>), grid, dim3(64 * 4), 0, st, rows, a.cosp, a.sinp, a.pos,
+                           a.kc, a.vc, ld, a.G, a);
 }
 
 template <bool FUSED>
@@ -918,6 +939,7 @@ extern "C" int bz_attn_step(const void* qkv, int64_t ld_qkv, int32_t B, int32_t 
                         split, workspace, out, ld_out);
     if (rc != BZ_OK) return rc;
     if (ld_qkv < (int64_t)(HQ + 2 * HKV) * D || ld_cs < 0) return BZ_ERR_SHAPE;
+    if (ld_qkv > 0x7FFFFFFF) return BZ_ERR_UNSUPPORTED;  // a preloaded 32-bit kernel argument
     a.qkv = static_cast<const uint16_t*>(qkv);
     a.ld_qkv = ld_qkv;
     a.qn = static_cast<const uint16_t*>(q_norm);
