@@ -206,8 +206,9 @@ __device__ __forceinline__ void i8_consume_unit(const GemvParams& p, StepCursor 
 }
 
 template <int WF, int MQ, int T, int D, bool SILU>
-__global__ void __launch_bounds__(kMaxThreads) gemv_i8mma(GemvParams p, int M) {
+__global__ void __launch_bounds__(kMaxThreads) gemv_i8mma(BZ_GEMV_HOT_PARAMS, GemvParams p, int M) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    gemv_hot(p, hx, hw, hsc0, hgamma, hldx, hrow_bytes, hK, hN, hntiles, htpw);
     const int nthr = blockDim.x;
     const int NW = nthr >> 6;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -305,7 +306,8 @@ template <int WF, int MQ, int T, int D, bool SILU>
 int launch_i8_kernel(const GemvParams& p, const Launch& l, hipStream_t st) {
     auto kern = gemv_i8mma<WF, MQ, T, D, SILU>;
     if (l.lds > 65536 && raise_lds_limit(reinterpret_cast<const void*>(kern)) != BZ_OK) return BZ_ERR_LAUNCH;
-    hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, p, l.M);
+    if (!gemv_hot_ok(p)) return BZ_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, BZ_GEMV_HOT_ARGS(p), p, l.M);
     return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }
 

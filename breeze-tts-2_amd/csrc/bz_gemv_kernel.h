@@ -86,6 +86,33 @@ struct GemvParams {
 
 __host__ __device__ constexpr int align16(int v) { return (v + 15) & ~15; }
 
+// The fields the first loads of the row-major kernels need, passed as
+// leading scalar kernel arguments so the hardware preloads them into SGPRs
+// at wave launch (kernarg preloading, -mllvm -amdgpu-kernarg-preload-count=16
+// in the build: 14 dwords; an aggregate is never preloaded).  The host
+// passes the same values in the struct.
+#define BZ_GEMV_HOT_PARAMS \
+    const uint16_t *hx, const uint8_t *hw, const void *hsc0, const uint16_t *hgamma, int hldx, int hrow_bytes, int hK, \
+        int hN, int hntiles, int htpw
+#define BZ_GEMV_HOT_ARGS(p) \
+    (p).x, (p).w, (p).sc0, (p).gamma, (int)(p).ldx, (int)(p).row_bytes, (p).K, (p).N, (p).ntiles, (p).tpw
+__device__ __forceinline__ void gemv_hot(GemvParams& p, const uint16_t* x, const uint8_t* w, const void* sc0,
+                                         const uint16_t* gamma, int ldx, int row_bytes, int K, int N, int ntiles,
+                                         int tpw) {
+    p.x = x;
+    p.w = w;
+    p.sc0 = sc0;
+    p.gamma = gamma;
+    p.ldx = ldx;
+    p.row_bytes = row_bytes;
+    p.K = K;
+    p.N = N;
+    p.ntiles = ntiles;
+    p.tpw = tpw;
+}
+// Host side: whether a GemvParams fits the 32-bit leading scalars.
+inline bool gemv_hot_ok(const GemvParams& p) { return p.ldx <= 0x7FFFFFFF && p.row_bytes <= 0x7FFFFFFF; }
+
 __host__ __device__ constexpr bool is_int4(int wf) { return wf == WF_I4ZP || wf == WF_I4MIN; }
 
 // Elements of one LDS x row: K rounded up to whole chunks.
@@ -597,8 +624,9 @@ __device__ __forceinline__ void consume_step(const GemvParams& p, StepCursor c, 
 
 // T = 2 for the SiLU-gate pair, else 1.  D = steps of loads in flight per wave.
 template <int WF, int M, int T, int D, bool SILU>
-__global__ void __launch_bounds__(kMaxThreads) gemv_persist(GemvParams p) {
+__global__ void __launch_bounds__(kMaxThreads) gemv_persist(BZ_GEMV_HOT_PARAMS, GemvParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    gemv_hot(p, hx, hw, hsc0, hgamma, hldx, hrow_bytes, hK, hN, hntiles, htpw);
     const int nthr = blockDim.x;
     const int NW = nthr >> 6;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -715,7 +743,8 @@ template <int WF, int M, int T, int D, bool SILU>
 int launch_persist(const GemvParams& p, const Launch& l, hipStream_t st) {
     auto kern = gemv_persist<WF, M, T, D, SILU>;
     if (l.lds > 65536 && raise_lds_limit(reinterpret_cast<const void*>(kern)) != BZ_OK) return BZ_ERR_LAUNCH;
-    hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, p);
+    if (!gemv_hot_ok(p)) return BZ_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, BZ_GEMV_HOT_ARGS(p), p);
     return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }
 

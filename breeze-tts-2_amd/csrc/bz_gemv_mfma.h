@@ -196,8 +196,9 @@ __device__ __forceinline__ void consume_unit(const GemvParams& p, StepCursor c, 
 
 // T = 2 for the SiLU-gate pair, else 1.  D = units of loads in flight per wave.
 template <int WF, int M, int T, int D, bool SILU>
-__global__ void __launch_bounds__(kMaxThreads) gemv_mfma(GemvParams p) {
+__global__ void __launch_bounds__(kMaxThreads) gemv_mfma(BZ_GEMV_HOT_PARAMS, GemvParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    gemv_hot(p, hx, hw, hsc0, hgamma, hldx, hrow_bytes, hK, hN, hntiles, htpw);
     const int nthr = blockDim.x;
     const int NW = nthr >> 6;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -263,7 +264,8 @@ template <int WF, int M, int T, int D, bool SILU>
 int launch_mfma_kernel(const GemvParams& p, const Launch& l, hipStream_t st) {
     auto kern = gemv_mfma<WF, M, T, D, SILU>;
     if (l.lds > 65536 && raise_lds_limit(reinterpret_cast<const void*>(kern)) != BZ_OK) return BZ_ERR_LAUNCH;
-    hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, p);
+    if (!gemv_hot_ok(p)) return BZ_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, BZ_GEMV_HOT_ARGS(p), p);
     return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }
 

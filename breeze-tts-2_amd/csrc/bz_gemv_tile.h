@@ -199,9 +199,25 @@ __device__ __forceinline__ void tile_sum_slices(const TileParams& tp, int cb, in
     }
 }
 
+// The fields the first loads need come as leading scalar arguments, which
+// the hardware preloads into SGPRs at wave launch (kernarg preloading, as
+// for the other GEMV kernels); the host passes the same values in the struct.
 template <int WF, int MB, int T, int D>
-__global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(TileParams tp) {
+__global__ void __launch_bounds__(kTileMaxThreads) gemv_tile(const uint16_t* hx, const uint8_t* hw, const void* hsc0,
+                                                             int hldx, int hrow_bytes, int hK, int hM, int hks, int hnsl,
+                                                             int hchunk, int hNU, TileParams tp) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    tp.p.x = hx;
+    tp.p.w = hw;
+    tp.p.sc0 = hsc0;
+    tp.p.ldx = hldx;
+    tp.p.row_bytes = hrow_bytes;
+    tp.p.K = hK;
+    tp.M = hM;
+    tp.ks = hks;
+    tp.nsl = hnsl;
+    tp.chunk = hchunk;
+    tp.NU = hNU;
     const GemvParams& p = tp.p;
     constexpr int UK = tile_unit_k(WF);
     constexpr int RS = 16 * MB;  // x128 row stride (rows per unit)
@@ -457,7 +473,9 @@ template <int WF, int MB, int T, int D>
 int launch_tile_kernel(const TileParams& tp, const TileLaunch& l, hipStream_t st) {
     auto kern = gemv_tile<WF, MB, T, D>;
     if (l.lds > 65536 && raise_lds_limit(reinterpret_cast<const void*>(kern)) != BZ_OK) return BZ_ERR_LAUNCH;
-    hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, tp);
+    if (tp.p.ldx > 0x7FFFFFFF || tp.p.row_bytes > 0x7FFFFFFF || tp.chunk > 0x7FFFFFFF) return BZ_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, tp.p.x, tp.p.w, tp.p.sc0, (int)tp.p.ldx,
+                       (int)tp.p.row_bytes, tp.p.K, tp.M, tp.ks, tp.nsl, (int)tp.chunk, tp.NU, tp);
     return hipGetLastError() == hipSuccess ? BZ_OK : BZ_ERR_LAUNCH;
 }
 
