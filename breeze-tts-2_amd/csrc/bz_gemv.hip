@@ -202,8 +202,10 @@ constexpr int kTileMinRows = 5;
 // (Tiled formats: unpaired weights only, and not with the second store;
 // not where the panel kernel is taken.)
 static bool panel_auto(const bz_gemv_desc* d);
+static bool stream_rows_auto(const bz_gemv_desc* d);
 static bool tile_auto(const bz_gemv_desc* d) {
-    return d->cfg_path == 0 && d->M >= kTileMinRows && !d->n_out2 && !tiled_paired(d->wfmt) && !panel_auto(d);
+    return d->cfg_path == 0 && d->M >= kTileMinRows && !d->n_out2 && !tiled_paired(d->wfmt) && !panel_auto(d) &&
+           !stream_rows_auto(d);
 }
 
 static int launch_tile(int wf, const TileParams& tp, const TileLaunch& l, hipStream_t st) {
@@ -291,10 +293,13 @@ static int wide_plan(const bz_gemv_desc* d, int rows, int T, WideLaunch& l) {
     if (T < 1 || T > kWideMaxBlocks) return BZ_ERR_INVALID_ARG;
     int nw = d->cfg_waves;
     if (nw < 0 || nw > kStreamMaxWaves) return BZ_ERR_INVALID_ARG;
-    const int per_wave = tiled_i4(wf) ? 2 : T > 1 ? 5 : 8;
+    const int mm = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+    // units per wave: int4 2, or 4 over more than 20 units with more than 2
+    // rows (int4 K4096 N2560 M = 5: 8 waves x 4 units 4.51 us, 16 x 2 4.74+);
+    // fp8 5 over several blocks, 8 over one
+    const int per_wave = tiled_i4(wf) ? (mm > 2 && NU > 20 ? 4 : 2) : T > 1 ? 5 : 8;
     if (!nw) nw = std::min(kStreamMaxWaves, (NU + per_wave - 1) / per_wave);
     const int need = (NU + nw - 1) / nw;
-    const int mm = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
     int upw = 0;
     for (int u : kWideUpw)
         if (u >= need && u <= wide_max_upw(wf, 1)) {
@@ -324,11 +329,24 @@ static int wide_plan(const bz_gemv_desc* d, int rows, int T, WideLaunch& l) {
 //     down K10240 N2560 7.43 -> 7.18 us, fp8 o_proj K4096 N2560 4.38 -> 4.13).
 //     Not fp8 qkv K2560 N4096 (one-block 3.92 us, several-block 4.02) nor the
 //     int4 rows of at most 256 blocks (int4 down K10240 N2560 5.69 against
-//     5.74, o_proj K4096 3.77 both).
-static int wide_rule(const bz_gemv_desc* d) {
+//     5.74, o_proj K4096 3.77 both);
+//   * 3 to 8 rows over rows of at most kWideShortK (one launch), unpaired and
+//     without RMSNorm (the cases measured): one block per workgroup where
+//     that plan fits.  At M = 3 / 4, against the one-block
+//     kernel: int4 K4096 N2560 4.21 / 4.40 -> 4.05 / 4.17 us, int4 K2560
+//     N4096 4.02 / 4.22 -> 3.90 / 3.98, fp8 K2560 N4096 4.38 / 4.41 -> 4.12
+//     / 4.18, fp8 K2048 N2048 3.57 / 3.71 -> 3.38 / 3.46 (int4 K2048 N2048
+//     3.36 / 3.49 -> 3.38 / 3.59: within the noise at the M = 3 it mostly
+//     sees).  At M = 5-8 see stream_rows_auto.
+constexpr int kWideShortK = 4096;
+static int wide_rule(const bz_gemv_desc* d, int rows) {
     const int nblk = d->N / 16, NU = tiled_units(d->wfmt, d->K);
     if (nblk > 256) return std::min(kWideMaxBlocks, (nblk + 255) / 256);
     if (!tiled_i4(d->wfmt) && NU >= 64) return 1;
+    if (rows >= 3 && d->K <= kWideShortK && !tiled_paired(d->wfmt) && !d->gamma) {
+        WideLaunch w{};
+        if (wide_plan(d, rows, 1, w) == BZ_OK) return 1;
+    }
     return 0;
 }
 
@@ -348,7 +366,7 @@ static int tiled_plan(const bz_gemv_desc* d, int rows, TiledPlan& pl) {
         if (d->cfg_tiles < 0 || d->cfg_tiles > kWideMaxBlocks) return BZ_ERR_INVALID_ARG;
         T = d->cfg_tiles;
     } else {
-        T = wide_rule(d);
+        T = wide_rule(d, rows);
         // a row too long for the several-block kernel's waves (int4 beyond
         // 16 x 5 units) stays on the one-block kernel
         if (T && wide_plan(d, rows, T, pl.w) == BZ_ERR_UNSUPPORTED && pl.w.upw == 0) T = 0;
@@ -413,39 +431,72 @@ static bool panel_ok(const bz_gemv_desc* d) {
 }
 
 // The automatic rule takes the panel kernel for them (measured on MI355X
-// against the streaming and tile kernels, int4 and fp8, N = 2560-20480,
+// against the streaming and tile kernels, int4 and fp8, N = 1024-20480,
 // K = 2560-10240, M = 2..32):
-//   * from 5 rows on, with K slices when the x of a launch exceeds
-//     kPanelSliceX (K = 10240 at M = 16, 32) and the workspace they need is
+//   * from 5 rows on, with K slices for rows of at least kPanelSliceMinK
+//     when the x of a launch exceeds kPanelSliceX or the weight has fewer
+//     than kPanelSliceFewBlocks row blocks, and the workspace they need is
 //     given (else over the whole K);
-//   * 3-4 rows of fp8 over at least 1280 row blocks (N >= 20480).
+//   * but not for 5-8 rows over rows of at most kWideShortK, which the
+//     several-block streaming kernel runs in one launch (stream_rows_auto).
 static bool panel_auto(const bz_gemv_desc* d) {
     if (d->cfg_path || !panel_ok(d)) return false;
-    const int M = d->M;
-    if (M >= 5) return true;
-    return M >= 3 && !tiled_i4(d->wfmt) && d->N / 16 >= 1280;
+    return d->M >= 5 && !stream_rows_auto(d);
+}
+
+// 5 to 8 rows of x over rows of at most kWideShortK: the streaming kernels
+// (wide_rule) in one launch, not the panel or tile kernel.  Measured on
+// MI355X (graph replays over >= 1 GiB of copies, us, M = 5 / 8; the panel
+// kernel's whole-K plan, then the several-block kernel):
+//   int4 K4096 N2560 5.61 / 5.62 -> 4.51 / 4.94, fp8 4.46 / 5.63 -> 4.55 / 4.69;
+//   int4 K2560 N4096 4.78 / 4.80 -> 4.29 / 4.75, fp8 5.32 / 5.07 -> 4.46 / 4.55;
+//   int4 K2560 N6144 6.46 / 6.44 -> 5.10 / 5.69, fp8 7.21 / 6.43 -> 5.13 / 5.17;
+//   int4 K2560 N20480 9.58 / 8.92 -> 8.18 / 8.95, fp8 11.33 / 10.83 -> 10.57 / 10.90;
+//   fp8 K2048 N2048 4.65 / 4.66 -> 3.60 / 3.60 (4 waves).
+// From 9 rows on the streaming kernels need two launches and the panel kernel
+// wins (int4 K4096 N2560 M = 12: 5.64 against 9.03).  The same 3-4 rows of
+// fp8 over 1280 blocks went to the panel kernel before: the several-block
+// kernel is faster there too (K2560 N20480 M = 3 / 4: 10.17 / 10.28 against
+// 10.3+ / 10.71).
+static bool stream_rows_auto(const bz_gemv_desc* d) {
+    return d->cfg_path == 0 && panel_ok(d) && d->M >= kTileMinRows && d->M <= kStreamMaxRows && d->K <= kWideShortK;
 }
 
 // x bytes of one launch above which the automatic rule splits K into slices
-// (every workgroup reads all of x over its K range from L2), the row blocks
-// per workgroup it takes then (int4, fp8) and the workgroups the slice count
-// aims for.  Measured on MI355X, K10240 N2560 (x of 320 / 640 KB at M = 16 /
-// 32), against the whole K and against the tile kernel's 128-column blocks
-// over 8-10 slices: int4 M = 32 2 blocks x 3 slices 12.7 us (whole K 13.9,
-// tile 13.4), M = 16 2 x 2 9.75 (10.0, 10.5); fp8 M = 32 3 blocks x 4 slices
-// 13.2 (tile 15.4), M = 16 3 x 4 10.6 (whole K 12.0).
-constexpr int64_t kPanelSliceX = 256 * 1024;
+// (every workgroup reads all of x over its K range from L2), the shortest
+// rows it splits, the most row blocks per workgroup it takes then (int4,
+// fp8; fewer for small N: one per kPanelSliceBlockRows blocks) and the
+// workgroups the slice count aims for.  Measured on MI355X (graph replays
+// over >= 1 GiB of weight copies, us):
+//   K10240 N2560, against the whole K and the tile kernel's 128-column
+//   blocks over 8-10 slices: int4 M = 32 2 blocks x 3 slices 12.7 (whole K
+//   13.9, tile 13.4), M = 16 2 x 2 9.75 (10.0, 10.5), M = 12 2 x 3 8.80
+//   (9.26); fp8 M = 32 3 x 4 13.2 (tile 15.4), M = 16 3 x 4 10.6 (whole K
+//   12.0), M = 12 3 x 4 10.1 (11.4), M = 8 3 x 4 9.81 (10.24);
+//   K8192 N1024 (64 blocks), sliced at every M since the whole K fills only
+//   64 CUs: fp8 M = 5 1 x 4 7.15 (whole K 7.61), M = 8 1 x 4 7.18 (7.94),
+//   M = 16 1 x 4 7.31 (9.51), M = 32 1 x 4 8.39 (3 x 11: 11.48); int4 M = 5
+//   1 x 4 7.02 (7.74), M = 8 7.08 (7.78), M = 16 1 x 4 7.06 (8.50), M = 32
+//   1 x 4 8.27 (3 x 11: 10.31);
+//   not for K <= 4096: K4096 N2560 and K2560 N4096 / N6144 at M = 16, 32
+//   run as fast or faster over the whole K (fp8 K4096 M = 32 8.10 against
+//   8.29 over 2 x 3).
+constexpr int64_t kPanelSliceX = 128 * 1024;
+constexpr int kPanelSliceMinK = 8192;
 constexpr int kPanelSliceBlocksI4 = 2, kPanelSliceBlocksF8 = 3;
+constexpr int kPanelSliceBlockRows = 48;
+constexpr int kPanelSliceFewBlocks = 128;  // fewer blocks: slices whatever the x bytes
 constexpr int kPanelTargetWorkgroups = 240;
 
 // Launch shape of the panel kernel (bz_gemv_panel.h) for `rows` <= 32 rows
-// of x: nsl K slices (cfg_slices; default 1 while the x of the launch is at
-// most kPanelSliceX, else about kPanelTargetWorkgroups workgroups in all), T
-// row blocks per workgroup (cfg_tiles: 1 to 5; default by the number of
-// blocks, or kPanelSliceBlocks* with slices), NW waves (cfg_waves; default
-// about 5 units per wave, 4 over K slices; at most 16 waves, 8 with several
-// blocks) splitting the slice's units UPW each.  `slices` > 0 overrides both the cfg and the
-// rule (1: no workspace).
+// of x: nsl K slices (cfg_slices; by default 1, or about
+// kPanelTargetWorkgroups workgroups in all where the rule above slices K and
+// that makes at least 2), T row blocks per workgroup (cfg_tiles: 1 to 5;
+// default by the number of blocks, or with the rule's slices
+// kPanelSliceBlocks* or fewer), NW waves (cfg_waves; default about 5 units
+// per wave, 4 over K slices and at least 8 over slices of one block; at most
+// 16 waves, 8 with several blocks) splitting the slice's units UPW each.
+// `slices` > 0 overrides both the cfg and the rule (1: no workspace).
 static int panel_plan(const bz_gemv_desc* d, int rows, PanelLaunch& l, int slices = 0) {
     const int wf = d->wfmt;
     if (tiled_paired(wf) || d->gamma || d->n_out2) return BZ_ERR_UNSUPPORTED;
@@ -455,9 +506,14 @@ static int panel_plan(const bz_gemv_desc* d, int rows, PanelLaunch& l, int slice
     const int nblk = d->N / 16;
     if (d->cfg_slices < 0) return BZ_ERR_INVALID_ARG;
     int nsl = slices ? slices : d->cfg_slices;
-    const bool rule_slices = !nsl && (int64_t)rows * d->K * 2 > kPanelSliceX;
-    const int T = d->cfg_tiles       ? d->cfg_tiles
-                  : rule_slices || nsl > 1 ? (tiled_i4(wf) ? kPanelSliceBlocksI4 : kPanelSliceBlocksF8)
+    const int slice_blocks =
+        std::max(1, std::min(tiled_i4(wf) ? kPanelSliceBlocksI4 : kPanelSliceBlocksF8, nblk / kPanelSliceBlockRows));
+    const int slice_groups = (nblk + slice_blocks - 1) / slice_blocks;
+    const bool rule_slices = !nsl && d->K >= kPanelSliceMinK &&
+                             ((int64_t)rows * d->K * 2 > kPanelSliceX || nblk < kPanelSliceFewBlocks) &&
+                             (kPanelTargetWorkgroups + slice_groups / 2) / slice_groups >= 2;
+    const int T = d->cfg_tiles                 ? d->cfg_tiles
+                  : rule_slices || nsl > 1 ? slice_blocks
                                            : panel_blocks(nblk);
     bool t_ok = false;
     for (int t : kPanelBlocks) t_ok |= t == T;
@@ -473,7 +529,9 @@ static int panel_plan(const bz_gemv_desc* d, int rows, PanelLaunch& l, int slice
     const int maxw = T == 1 ? kPanelMaxWaves : 8;
     int nw = d->cfg_waves;
     if (nw < 0 || nw > maxw) return BZ_ERR_INVALID_ARG;
-    if (!nw) nw = std::min(maxw, nsl > 1 ? (ups + 3) / 4 : (ups + 4) / 5);  // sliced: int4 M = 16 7 x 4 units 9.25 us, 6 x 5 9.78
+    // sliced: int4 K10240 M = 16 7 waves x 4 units 9.25 us, 6 x 5 9.78; one
+    // block over K8192 slices of 16 units: int4 M = 32 8 x 2 8.27, 4 x 4 8.6+
+    if (!nw) nw = std::min(maxw, nsl > 1 ? std::max((ups + 3) / 4, T == 1 ? 8 : 1) : (ups + 4) / 5);
     const int need = (ups + nw - 1) / nw;
     int upw = 0;
     for (int u : kPanelUpw)
@@ -645,10 +703,6 @@ extern "C" int bz_gemv(const bz_gemv_desc* d, void* stream) {
             return BZ_OK;
         }
     }
-    // several rows of a tiled weight the tile kernel did not take (no
-    // workspace): the panel kernel, which needs none
-    if (tiled && d->cfg_path == 0 && M >= kTileMinRows && panel_ok(d))
-        return gemv_panel_rows(d, static_cast<hipStream_t>(stream));
     if (tiled) return gemv_tiled(d, di, static_cast<hipStream_t>(stream));
 
     const bool silu = epi == BZ_EPI_SILU_GATE;

@@ -151,10 +151,11 @@ typedef enum bz_dtype {
  * (BZ_W_INT4_TILED, BZ_W_FP8_TILED), no RMSNorm, epilogue NONE or RESIDUAL,
  * no second store: each workgroup of cfg_waves waves (0: about 5 units per
  * wave; at most 16, or 8 with several blocks) covers cfg_tiles consecutive
- * 16-row blocks (1..5; 0: enough to keep about 256 workgroups, or 2 (int4)
- * / 3 (fp8) with K slices) over the whole K or over one of cfg_slices K
- * slices (0: one while the x of a launch is at most 256 KB, else about 240
- * workgroups in all); larger M runs 32 rows per launch.  With more than
+ * 16-row blocks (1..5; 0: enough to keep about 256 workgroups, or with K
+ * slices 2 (int4) / 3 (fp8), one per 48 blocks for fewer) over the whole K
+ * or over one of cfg_slices K slices (0: one, or, for K >= 8192 with more
+ * than 128 KB of x per launch or N < 2048, about 240 workgroups in all
+ * where that makes at least two slices); larger M runs 32 rows per launch.  With more than
  * one slice the slices' fp32 sums go to `workspace` as for path 4
  * (bz_gemv_workspace bytes); forced slices without it return
  * BZ_ERR_INVALID_ARG, and the rule's slices without it fall back to the

@@ -159,8 +159,9 @@ def test_panel_full_size(fmt, n, k, m):
 
 def test_panel_automatic_choice():
     """The built-in rule takes the panel kernel (bit-identical to forcing it)
-    from 5 rows on, and for fp8 at 3-4 rows over >= 1280 row blocks; not for
-    int4 at 3 rows (another path: same result within the bar)."""
+    from 5 rows on, except 5-8 rows over K <= 4096 (one launch of the
+    streaming kernel); not at 3 rows (another path: same result within the
+    bar)."""
     from breeze_amd import tuning
 
     saved = dict(tuning._TABLES)
@@ -168,8 +169,10 @@ def test_panel_automatic_choice():
     tuning._TABLES[tuning.arch_of(torch.device("cuda"))] = {}  # the built-in rule, not the table
     try:
         for fmt, n, k, m, panel in [("int4", 2560, 10240, 16, True), ("int4", 2560, 4096, 32, True),
-                                    ("fp8", 20480, 2560, 3, True), ("int4", 2560, 10240, 32, True),
-                                    ("fp8", 2560, 10240, 32, True), ("int4", 20480, 2560, 3, False)]:
+                                    ("fp8", 20480, 2560, 3, False), ("int4", 2560, 10240, 32, True),
+                                    ("fp8", 2560, 10240, 32, True), ("int4", 20480, 2560, 3, False),
+                                    ("int4", 2560, 4096, 8, False), ("fp8", 4096, 2560, 5, False),
+                                    ("fp8", 2560, 10240, 8, True), ("int4", 2048, 2048, 12, True)]:
             buf, wf, w_eff = _weight(fmt, n, k, 600 + m)
             x = _x(m, k, 601)
             auto = _run(buf, wf, n, x, cfg=(0, 0, 0, 0))
@@ -309,16 +312,34 @@ def test_panel_slices_match_oracle_and_whole_k(fmt, n, k, m, blocks, slices):
                                 out_dtype=out_dtype), got)
 
 
-def test_panel_rule_slices_at_full_size():
-    """K10240 N2560 at M = 32: the rule's slices (int4 2 blocks x 3 slices,
-    fp8 3 x 4) are what the automatic call runs, bit for bit."""
-    for fmt, blocks, slices in (("int4", 2, 3), ("fp8", 3, 4)):
-        buf, wf, w_eff = _weight(fmt, 2560, 10240, 1200)
-        x = _x(32, 10240, 1201)
-        auto = _run(buf, wf, 2560, x, cfg=(0, 0, 0, 0))
-        forced = _run(buf, wf, 2560, x, cfg=(0, 0, blocks, PANEL, slices))
-        assert torch.equal(auto, forced), fmt
-        assert O.rel_err(f32(auto), _ref(x, w_eff)) <= TIGHT
+@pytest.mark.parametrize(
+    "fmt,n,k,m,blocks,slices",
+    [
+        ("int4", 2560, 10240, 32, 2, 3),   # the C4 down shape
+        ("fp8", 2560, 10240, 32, 3, 4),
+        ("fp8", 2560, 10240, 8, 3, 4),     # 160 KB of x
+        ("int4", 2560, 10240, 12, 2, 3),
+        ("fp8", 1024, 8192, 16, 1, 4),     # 64 blocks: one per workgroup
+        ("int4", 1024, 8192, 32, 1, 4),
+        ("fp8", 1024, 8192, 5, 1, 4),      # 80 KB of x, but only 64 blocks
+        ("int4", 2560, 10240, 6, 5, 1),    # 120 KB of x: the whole K
+        ("fp8", 2560, 4096, 32, 5, 1),     # K below 8192: the whole K
+        ("int4", 20480, 2560, 32, 5, 1),   # K2560 N20480: the whole K, 5 blocks
+    ],
+)
+def test_panel_rule_slices_at_full_size(fmt, n, k, m, blocks, slices):
+    """The rule's K slices and blocks per workgroup are what the automatic
+    call runs, bit for bit (with `blocks` = 5 and one slice standing for the
+    whole-K plan, whose blocks per workgroup follow from N)."""
+    buf, wf, w_eff = _weight(fmt, n, k, 1200)
+    x = _x(m, k, 1201)
+    auto = _run(buf, wf, n, x, cfg=(0, 0, 0, 0))
+    if slices == 1:
+        forced = _run(buf, wf, n, x, cfg=(0, 0, 0, PANEL, 1))
+    else:
+        forced = _run(buf, wf, n, x, cfg=(0, 0, blocks, PANEL, slices))
+    assert torch.equal(auto, forced), (fmt, n, k, m)
+    assert O.rel_err(f32(auto), _ref(x, w_eff)) <= TIGHT
 
 
 def test_panel_slices_graph_replays_match_eager():

@@ -413,8 +413,9 @@ def test_tile_kernel_reads_tiled_formats(fmt, m):
     """The several-row tile kernel (path 4) reads a tiled weight in place: the
     result is bit-identical to the same kernel over the row-major weight
     (same launch plan, same arithmetic) and within the bar of the oracle.
-    The automatic choice for this shape (min(M, 32) K <= 196608) is the panel kernel
-    (path 6)."""
+    The automatic choice for this shape is the several-block streaming kernel
+    with one block per workgroup up to 8 rows (one launch) and the panel
+    kernel (path 6) beyond."""
     n, k = 2560, 2560
     c = _int4_case(n, k, 950 + m) if fmt == "int4" else _fp8_case(n, k, 960 + m)
     tbuf, tf = _tiled_i4(c, False) if fmt == "int4" else _tiled_f8(c, False)
@@ -433,8 +434,11 @@ def test_tile_kernel_reads_tiled_formats(fmt, m):
     auto = G.gemv(bf16_tensor(x), tbuf, tf, n, epilogue=G.EPI_RESIDUAL, residual=bf16_tensor(res))
     panel = G.gemv(bf16_tensor(x), tbuf, tf, n, epilogue=G.EPI_RESIDUAL, residual=bf16_tensor(res),
                    cfg=(0, 0, 0, 6))
-    assert torch.equal(auto, panel)   # the automatic choice from M = 5 on
+    wide = G.gemv(bf16_tensor(x), tbuf, tf, n, epilogue=G.EPI_RESIDUAL, residual=bf16_tensor(res),
+                  cfg=(0, 0, 1, 5))
+    assert torch.equal(auto, wide if m <= 8 else panel)
     assert O.rel_err(f32(panel), _ref(x, w_eff, None, O.EPI_RES, res)) <= TIGHT
+    assert O.rel_err(f32(wide), _ref(x, w_eff, None, O.EPI_RES, res)) <= TIGHT
     assert O.rel_err(f32(got), _ref(x, w_eff, None, O.EPI_RES, res)) <= TIGHT
 
 
@@ -580,6 +584,42 @@ def test_gemv_wide_rule_at_full_size():
         assert torch.equal(auto, forced), (fmt, n)
         w_eff = c.w_zp if fmt == "int4" else c.w_eff
         assert O.rel_err(f32(auto), _ref(x, w_eff, g, epi, None)) <= TIGHT
+
+
+@pytest.mark.parametrize(
+    "fmt,n,k,m,T",
+    [
+        ("int4", 2560, 4096, 3, 1),    # one block per workgroup from 3 rows over K <= 4096
+        ("fp8", 4096, 2560, 4, 1),
+        ("int4", 2560, 4096, 5, 1),    # 5-8 rows: one streaming launch, not the panel kernel
+        ("fp8", 4096, 2560, 8, 1),
+        ("fp8", 2048, 2048, 6, 1),
+        ("int4", 6144, 2560, 7, 2),    # more than 256 blocks: the block count of the rule
+        ("fp8", 20480, 2560, 3, 5),    # no longer the panel kernel at 3-4 rows
+        ("int4", 20480, 2560, 8, 5),
+    ],
+)
+def test_gemv_wide_rule_several_rows(fmt, n, k, m, T):
+    """From 3 to 8 rows over rows of K <= 4096 (unpaired, no RMSNorm) the
+    built-in rule runs the several-block kernel in one launch: the automatic
+    result equals the one forced with the rule's block count bit for bit."""
+    from breeze_amd import tuning
+
+    saved = dict(tuning._TABLES)
+    tuning._TABLES.clear()
+    tuning._TABLES[tuning.arch_of(torch.device("cuda"))] = {}  # the built-in rule, not the table
+    try:
+        c = _int4_case(n, k, 750) if fmt == "int4" else _fp8_case(n, k, 751)
+        buf, tf = _tiled_i4(c, False) if fmt == "int4" else _tiled_f8(c, False)
+        x = _x(m, k, 752)
+        auto = G.gemv(bf16_tensor(x), buf, tf, n)
+        forced = G.gemv(bf16_tensor(x), buf, tf, n, cfg=(0, 0, T, 5))
+        assert torch.equal(auto, forced), (fmt, n, k, m)
+        w_eff = c.w_zp if fmt == "int4" else c.w_eff
+        assert O.rel_err(f32(auto), _ref(x, w_eff, None, 0, None)) <= TIGHT
+    finally:
+        tuning._TABLES.clear()
+        tuning._TABLES.update(saved)
 
 
 def test_gemv_wide_rejects_bad_block_counts():
