@@ -1,6 +1,6 @@
 """Offline launch-shape sweep that writes the static table read by tuning.py.
 
-    python -m breeze_amd.tune [--out PATH] [--budget-mb 512]
+    python -m breeze_amd.tune [--out PATH] [--budget-mb 512] [--only NAME] [--tiled-decode] [--merge]
 
 Run once per GPU architecture (the reference instead tunes at install time,
 models/fused/kernels.py:262-286, and persists per GPU name, :289-331).  Each
@@ -9,8 +9,9 @@ configurations is timed at M = 1 and 2, and the several-row shapes at
 M = 4..32, as HIP-graph replays over rotating weight copies (so the weights
 stream from HBM, not the 256 MB Infinity Cache), for the built-in rule and a
 grid of (depth, waves, tiles, path[, slices]); the int4 / fp8 decode shapes
-are also timed in the tiled decode layout (the streaming kernel, path 5) over
-its wave counts.  An entry is written only where the best shape beats the
+are also timed in the tiled decode layout (the streaming kernels, path 5) over
+the one-block kernel's wave counts and the several-block kernel's blocks per
+workgroup and wave counts.  An entry is written only where the best shape beats the
 built-in rule by at least --min-gain.  Every candidate is validated against
 the built-in rule's output before it is timed; the rule is timed once before
 its measured run (the first timing of a shape reads high), and the rule and
@@ -66,12 +67,14 @@ ROW_CANDIDATES = [(0, 0, 0, 2), (0, 0, 0, 3)] + [
 
 # The tiled decode layout: the int4 / fp8 shapes above, plus the down and o
 # projections without an epilogue (as the benchmark's configuration rows time
-# them); wave counts of the streaming kernel.
+# them); wave counts of the one-block streaming kernel (cfg_tiles 0) and of the
+# several-block kernel over 1-8 row blocks per workgroup.
 TILED_SHAPES = [s for s in SHAPES if s[1] != "bf16"] + [
     ("C2 down, no epi", "int4", 2560, 10240, 0, False), ("C3 o, no epi", "fp8", 2560, 4096, 0, False),
     ("C3 down, no epi", "fp8", 2560, 10240, 0, False), ("C5 o, no epi", "int4", 2560, 4096, 0, False),
 ]
-TILED_CANDIDATES = [(0, w, 0, 5) for w in (2, 3, 4, 5, 6, 7, 8, 10, 11, 12, 14, 16)]
+TILED_CANDIDATES = [(0, w, 0, 5) for w in (2, 3, 4, 5, 6, 7, 8, 10, 11, 12, 14, 16)] + [
+    (0, w, t, 5) for t in (1, 2, 3, 4, 5, 6, 8) for w in (2, 4, 6, 8, 10, 12, 16)]
 # The panel kernel (several rows over the tiled layout): row blocks per
 # workgroup and wave counts.
 PANEL_CANDIDATES = [(0, w, t, 6) for t in (1, 2, 3, 4, 5) for w in (4, 5, 8, 10, 16) if w <= (16 if t == 1 else 8)]
@@ -99,19 +102,22 @@ def _weights(fmt, N, K, dev, tiled=False, paired=False):
     return dict(w=b, wfmt=G.W_BF16), 2 * b.numel()
 
 
-def sweep(budget_mb: int, min_gain: float, log=print, only: str = "") -> dict:
+def sweep(budget_mb: int, min_gain: float, log=print, only: str = "", tiled_decode: bool = False) -> dict:
     dev = torch.device("cuda", torch.cuda.current_device())
     arch = tuning.arch_of(dev)
     table = {}
     jobs = [(name, fmt, N, K, epi, norm, (1, 2), CANDIDATES, False) for name, fmt, N, K, epi, norm in SHAPES]
     jobs += [(name, fmt, N, K, 0, False, ROW_MS, ROW_CANDIDATES, False) for name, fmt, N, K in ROW_SHAPES]
-    jobs += [(name + " tiled", fmt, N, K, epi, norm, (1, 2), TILED_CANDIDATES, True)
-             for name, fmt, N, K, epi, norm in TILED_SHAPES]
+    tiled_jobs = [(name + " tiled", fmt, N, K, epi, norm, (1, 2), TILED_CANDIDATES, True)
+                  for name, fmt, N, K, epi, norm in TILED_SHAPES]
+    jobs += tiled_jobs
     # the several-row shapes in the tiled layout: the tile kernel reads it in
     # place, and the panel kernel
     jobs += [(name + " tiled", fmt, N, K, 0, False, ROW_MS,
               [c for c in ROW_CANDIDATES if c[3] == 4] + PANEL_CANDIDATES, True)
              for name, fmt, N, K in ROW_SHAPES]
+    if tiled_decode:
+        jobs = tiled_jobs
     if only:
         jobs = [j for j in jobs if only in j[0]]
     swept = []
@@ -179,10 +185,13 @@ def main(argv=None) -> int:
     ap.add_argument("--budget-mb", type=int, default=512, help="rotating weight copies per shape")
     ap.add_argument("--min-gain", type=float, default=0.03, help="keep entries at least this much faster")
     ap.add_argument("--only", default="", help="sweep only the shapes whose name contains this")
+    ap.add_argument("--tiled-decode", action="store_true",
+                    help="sweep only the decode shapes (M = 1, 2) in the tiled layout")
     ap.add_argument("--merge", action="store_true",
                     help="update the existing table: replace the swept keys' entries, keep the others")
     args = ap.parse_args(argv)
-    res = sweep(args.budget_mb, args.min_gain, log=lambda s: print(s, flush=True), only=args.only)
+    res = sweep(args.budget_mb, args.min_gain, log=lambda s: print(s, flush=True), only=args.only,
+                tiled_decode=args.tiled_decode)
     path = args.out or str(tuning.table_path(res["arch"]))
     table = res["table"]
     if args.merge:

@@ -41,8 +41,10 @@ def test_committed_table_entries_are_valid_shapes():
             assert int(wfmt) in (4, 6) and not int(norm) and int(epi) in (0, 2) and depth == 0
             assert 1 <= tiles <= 5 and 0 <= waves <= (16 if tiles == 1 else 8) and len(cfg) == 4
             continue
-        if path == 5:  # the streaming kernel of the tiled formats: only the wave count is read
-            assert int(wfmt) in (4, 5, 6, 7) and 1 <= waves <= 16 and depth == 0 and tiles == 0 and len(cfg) == 4
+        if path == 5:  # the streaming kernels of the tiled formats: the wave count, and the row
+            # blocks per workgroup (0: the one-block kernel, 1-8: the several-block kernel)
+            assert int(wfmt) in (4, 5, 6, 7) and 1 <= waves <= 16 and depth == 0 and 0 <= tiles <= 8
+            assert len(cfg) == 4
             continue
         # row-major formats; path 4 also reads the unpaired tiled ones in place
         assert int(wfmt) in (0, 1, 2, 3) or (path == 4 and int(wfmt) in (4, 6))
