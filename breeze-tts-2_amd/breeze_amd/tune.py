@@ -1,6 +1,6 @@
 """Offline launch-shape sweep that writes the static table read by tuning.py.
 
-    python -m breeze_amd.tune [--out PATH] [--budget-mb 512] [--only NAME] [--tiled-decode] [--merge]
+    python -m breeze_amd.tune [--out PATH] [--budget-mb 512] [--only NAME] [--tiled-decode [--ms 4,8]] [--merge]
 
 Run once per GPU architecture (the reference instead tunes at install time,
 models/fused/kernels.py:262-286, and persists per GPU name, :289-331).  Each
@@ -102,13 +102,14 @@ def _weights(fmt, N, K, dev, tiled=False, paired=False):
     return dict(w=b, wfmt=G.W_BF16), 2 * b.numel()
 
 
-def sweep(budget_mb: int, min_gain: float, log=print, only: str = "", tiled_decode: bool = False) -> dict:
+def sweep(budget_mb: int, min_gain: float, log=print, only: str = "", tiled_decode: bool = False,
+          ms: tuple = ()) -> dict:
     dev = torch.device("cuda", torch.cuda.current_device())
     arch = tuning.arch_of(dev)
     table = {}
     jobs = [(name, fmt, N, K, epi, norm, (1, 2), CANDIDATES, False) for name, fmt, N, K, epi, norm in SHAPES]
     jobs += [(name, fmt, N, K, 0, False, ROW_MS, ROW_CANDIDATES, False) for name, fmt, N, K in ROW_SHAPES]
-    tiled_jobs = [(name + " tiled", fmt, N, K, epi, norm, (1, 2), TILED_CANDIDATES, True)
+    tiled_jobs = [(name + " tiled", fmt, N, K, epi, norm, ms or (1, 2), TILED_CANDIDATES, True)
                   for name, fmt, N, K, epi, norm in TILED_SHAPES]
     jobs += tiled_jobs
     # the several-row shapes in the tiled layout: the tile kernel reads it in
@@ -186,12 +187,13 @@ def main(argv=None) -> int:
     ap.add_argument("--min-gain", type=float, default=0.03, help="keep entries at least this much faster")
     ap.add_argument("--only", default="", help="sweep only the shapes whose name contains this")
     ap.add_argument("--tiled-decode", action="store_true",
-                    help="sweep only the decode shapes (M = 1, 2) in the tiled layout")
+                    help="sweep only the decode shapes in the tiled layout")
+    ap.add_argument("--ms", default="", help="rows of the tiled decode shapes (default 1,2; e.g. 4,8 for MTP + CFG)")
     ap.add_argument("--merge", action="store_true",
                     help="update the existing table: replace the swept keys' entries, keep the others")
     args = ap.parse_args(argv)
     res = sweep(args.budget_mb, args.min_gain, log=lambda s: print(s, flush=True), only=args.only,
-                tiled_decode=args.tiled_decode)
+                tiled_decode=args.tiled_decode, ms=tuple(int(m) for m in args.ms.split(",") if m))
     path = args.out or str(tuning.table_path(res["arch"]))
     table = res["table"]
     if args.merge:

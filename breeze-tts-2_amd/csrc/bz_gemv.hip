@@ -337,8 +337,9 @@ static int wide_plan(const bz_gemv_desc* d, int rows, int T, WideLaunch& l) {
 //     N4096 4.02 / 4.22 -> 3.90 / 3.98, fp8 K2560 N4096 4.38 / 4.41 -> 4.12
 //     / 4.18, fp8 K2048 N2048 3.57 / 3.71 -> 3.38 / 3.46 (int4 K2048 N2048
 //     3.36 / 3.49 -> 3.38 / 3.59: within the noise at the M = 3 it mostly
-//     sees).  At M = 5-8 see stream_rows_auto.
-constexpr int kWideShortK = 4096;
+//     sees); int4 K6144 N2048 (+ residual) M = 4 5.19 -> 5.00.  At M = 5-8 see
+//     stream_rows_auto.
+constexpr int kWideShortK = 8192;
 static int wide_rule(const bz_gemv_desc* d, int rows) {
     const int nblk = d->N / 16, NU = tiled_units(d->wfmt, d->K);
     if (nblk > 256) return std::min(kWideMaxBlocks, (nblk + 255) / 256);
@@ -453,13 +454,22 @@ static bool panel_auto(const bz_gemv_desc* d) {
 //   int4 K2560 N6144 6.46 / 6.44 -> 5.10 / 5.69, fp8 7.21 / 6.43 -> 5.13 / 5.17;
 //   int4 K2560 N20480 9.58 / 8.92 -> 8.18 / 8.95, fp8 11.33 / 10.83 -> 10.57 / 10.90;
 //   fp8 K2048 N2048 4.65 / 4.66 -> 3.60 / 3.60 (4 waves).
-// From 9 rows on the streaming kernels need two launches and the panel kernel
-// wins (int4 K4096 N2560 M = 12: 5.64 against 9.03).  The same 3-4 rows of
-// fp8 over 1280 blocks went to the panel kernel before: the several-block
-// kernel is faster there too (K2560 N20480 M = 3 / 4: 10.17 / 10.28 against
-// 10.3+ / 10.71).
+//   and up to K8192, against the panel kernel (+ residual, M = 8): int4 K6144
+//   N2048 7.26 -> 6.01, fp8 K8192 N1024 (over 4 K slices) 7.72 -> 6.00.
+// Over K10240 the panel kernel's K slices win (fp8 M = 8: 10.23 against the
+// several-block kernel's 16 waves x 10 units; int4 does not fit the waves
+// at 8 rows).  Only where the several-block plan runs all the rows in one
+// launch.  From 9 rows on the streaming kernels need two launches and the
+// panel kernel wins (int4 K4096 N2560 M = 12: 5.64 against 9.03).  The same
+// 3-4 rows of fp8 over 1280 blocks went to the panel kernel before: the
+// several-block kernel is faster there too (K2560 N20480 M = 3 / 4: 10.17 /
+// 10.28 against 10.3+ / 10.71).
 static bool stream_rows_auto(const bz_gemv_desc* d) {
-    return d->cfg_path == 0 && panel_ok(d) && d->M >= kTileMinRows && d->M <= kStreamMaxRows && d->K <= kWideShortK;
+    if (d->cfg_path != 0 || !panel_ok(d) || d->M < kTileMinRows || d->M > kStreamMaxRows || d->K > kWideShortK)
+        return false;
+    const int T = wide_rule(d, d->M);
+    WideLaunch w{};
+    return T > 0 && wide_plan(d, d->M, T, w) == BZ_OK;
 }
 
 // x bytes of one launch above which the automatic rule splits K into slices

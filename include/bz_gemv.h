@@ -129,8 +129,9 @@ typedef enum bz_dtype {
  * waves per workgroup (0 = the kernel's rule), cfg_depth unused; 6 = the
  * several-row panel kernel of the tiled formats, see below).  Without a cfg
  * the rule takes the several-block kernel for weights of more than 256 row
- * blocks (one workgroup per CU) and for fp8 rows of 64 units or more.
- * Used by tuning sweeps.
+ * blocks (one workgroup per CU), for fp8 rows of 64 units or more, and for
+ * 3-8 rows of an unpaired weight without RMSNorm over K <= 8192 (one block
+ * per workgroup, all rows in one launch).  Used by tuning sweeps.
  *
  * Several rows (path 4).  Up to 32 rows of x per launch stream every weight
  * byte once: a workgroup of cfg_waves waves (4 or 8) owns 16 * cfg_tiles
@@ -160,8 +161,8 @@ typedef enum bz_dtype {
  * (bz_gemv_workspace bytes); forced slices without it return
  * BZ_ERR_INVALID_ARG, and the rule's slices without it fall back to the
  * whole K.  The automatic rule takes this path for these weights from M = 5
- * on, and for fp8 at M = 3-4 with N >= 20480; the streaming kernels
- * otherwise.
+ * on, except 5-8 rows over K <= 8192 that the several-block streaming
+ * kernel runs in one launch; the streaming kernels otherwise.
  */
 typedef struct bz_gemv_desc {
     int32_t abi_version;      /* must be BZ_ABI_VERSION */

@@ -589,7 +589,7 @@ def test_gemv_wide_rule_at_full_size():
 @pytest.mark.parametrize(
     "fmt,n,k,m,T",
     [
-        ("int4", 2560, 4096, 3, 1),    # one block per workgroup from 3 rows over K <= 4096
+        ("int4", 2560, 4096, 3, 1),    # one block per workgroup from 3 rows over K <= 8192
         ("fp8", 4096, 2560, 4, 1),
         ("int4", 2560, 4096, 5, 1),    # 5-8 rows: one streaming launch, not the panel kernel
         ("fp8", 4096, 2560, 8, 1),
@@ -597,10 +597,13 @@ def test_gemv_wide_rule_at_full_size():
         ("int4", 6144, 2560, 7, 2),    # more than 256 blocks: the block count of the rule
         ("fp8", 20480, 2560, 3, 5),    # no longer the panel kernel at 3-4 rows
         ("int4", 20480, 2560, 8, 5),
+        ("int4", 2048, 6144, 4, 1),    # K up to 8192
+        ("int4", 2048, 6144, 8, 1),
+        ("fp8", 1024, 8192, 6, 1),
     ],
 )
 def test_gemv_wide_rule_several_rows(fmt, n, k, m, T):
-    """From 3 to 8 rows over rows of K <= 4096 (unpaired, no RMSNorm) the
+    """From 3 to 8 rows over rows of K <= 8192 (unpaired, no RMSNorm) the
     built-in rule runs the several-block kernel in one launch: the automatic
     result equals the one forced with the rule's block count bit for bit."""
     from breeze_amd import tuning
