@@ -280,6 +280,33 @@ def test_gemv_tiled_f32_out_and_residual():
     assert O.rel_err(f32(out), ref) <= TOL
 
 
+@pytest.mark.parametrize(
+    "fmt,n,k,m",
+    [
+        ("int4", 2048, 6144, 3), ("int4", 2048, 6144, 7), ("int4", 1024, 8192, 8),
+        ("fp8", 1024, 8192, 5), ("fp8", 2560, 4096, 7), ("fp8", 1536, 1024, 6),
+    ],
+)
+def test_gemv_several_rows_streaming_residual_f32(fmt, n, k, m):
+    """Several rows over K <= 8192 on the automatic path (the several-block
+    kernel in one launch, ragged row counts included) with an fp32 residual
+    and fp32 output, against the oracle; the same call with a bf16 residual
+    and output agrees to the bf16 bar."""
+    c = _int4_case(n, k, 760 + m) if fmt == "int4" else _fp8_case(n, k, 761 + m)
+    buf, tf = _tiled_i4(c, False) if fmt == "int4" else _tiled_f8(c, False)
+    w_eff = c.w_zp if fmt == "int4" else c.w_eff
+    x_bits = _x(m, k, 762 + m)
+    res = torch.randn(m, n, device="cuda", dtype=torch.float32)
+    out = G.gemv(bf16_tensor(x_bits), buf, tf, n, epilogue=G.EPI_RESIDUAL, residual=res, out_dtype=torch.float32)
+    assert out.dtype == torch.float32
+    ref = O.gemv_ref(O.bf16_bits_to_f32(x_bits), w_eff, O.EPI_RES, res.cpu().numpy())
+    assert O.rel_err(f32(out), ref) <= TOL
+    res16 = res.to(torch.bfloat16)
+    out16 = G.gemv(bf16_tensor(x_bits), buf, tf, n, epilogue=G.EPI_RESIDUAL, residual=res16)
+    ref16 = O.gemv_ref(O.bf16_bits_to_f32(x_bits), w_eff, O.EPI_RES, res16.float().cpu().numpy())
+    assert O.rel_err(f32(out16), ref16) <= TIGHT
+
+
 def test_gemv_tiled_rejects_wrong_epilogue_and_size():
     n, k = 64, 256
     c = _int4_case(n, k, 95)
