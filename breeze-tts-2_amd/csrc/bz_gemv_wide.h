@@ -62,7 +62,10 @@ constexpr int kWideUpw[] = {2, 3, 4, 5, 6, 8, 10};
 __host__ __device__ constexpr int wide_max_upw(int wf, int mm) { return tiled_i4(wf) ? (mm <= 2 ? 5 : 4) : 10; }
 constexpr int kWideMaxBlocks = 8;
 
-template <int WF, int MM, int UPW>
+// TC > 0: the row blocks per workgroup fixed at compile time (every
+// workgroup takes exactly TC, the host checks that TC divides the blocks), so
+// the block loop unrolls completely; TC = 0 takes T at run time.
+template <int WF, int MM, int UPW, int TC = 0>
 __global__ void __launch_bounds__(1024) gemv_wide(const uint8_t* hw, const uint16_t* hx, const uint16_t* hg, int hchunk,
                                                   int hldx, int hK, int hNU, int hM, int hnorm, int T, int nblk,
                                                   StreamParams p) {
@@ -78,8 +81,9 @@ __global__ void __launch_bounds__(1024) gemv_wide(const uint8_t* hw, const uint1
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 15, kq = lane >> 4;
     const int M = p.M, K = p.K, NU = p.NU;
+    if constexpr (TC > 0) T = TC;
     const int b0 = blockIdx.x * T;
-    const int nb = min(T, nblk - b0);
+    const int nb = TC > 0 ? TC : min(T, nblk - b0);
     const int ocols = PAIR ? 8 : 16;
 
     const WideLds L = wide_lds(WF, M, K, T);
@@ -295,12 +299,21 @@ __global__ void __launch_bounds__(1024) gemv_wide(const uint8_t* hw, const uint1
     // pairs of blocks without a branch inside (a conditional second half made
     // the loop's two paths leave different registers with loads in flight,
     // and the compiler then waited for all of them), then an odd last block
-    int jb = 0;
-    for (; jb + 1 < nb; jb += 2) {
-        run_block(jb, wa, sa, wb, sb);
-        run_block(jb + 1, wb, sb, wa, sa);
+    if constexpr (TC > 0) {
+#pragma unroll
+        for (int jb = 0; jb + 1 < TC; jb += 2) {
+            run_block(jb, wa, sa, wb, sb);
+            run_block(jb + 1, wb, sb, wa, sa);
+        }
+        if constexpr ((TC & 1) != 0) run_block(TC - 1, wa, sa, wb, sb);
+    } else {
+        int jb = 0;
+        for (; jb + 1 < nb; jb += 2) {
+            run_block(jb, wa, sa, wb, sb);
+            run_block(jb + 1, wb, sb, wa, sa);
+        }
+        if (jb < nb) run_block(jb, wa, sa, wb, sb);
     }
-    if (jb < nb) run_block(jb, wa, sa, wb, sb);
     __syncthreads();
 
     // 3. one lane per output: its 16 wave slots added in wave order, then the
@@ -358,9 +371,9 @@ struct WideLaunch {
     size_t lds;
 };
 
-template <int WF, int MM, int UPW>
+template <int WF, int MM, int UPW, int TC = 0>
 int launch_wide_kernel(const StreamParams& p, const WideLaunch& l, int nblk, hipStream_t st) {
-    auto kern = gemv_wide<WF, MM, UPW>;
+    auto kern = gemv_wide<WF, MM, UPW, TC>;
     if (l.lds > 65536 && raise_lds_limit(reinterpret_cast<const void*>(kern)) != BZ_OK) return BZ_ERR_LAUNCH;
     if (!stream_hot_ok(p)) return BZ_ERR_UNSUPPORTED;
     hipLaunchKernelGGL(kern, dim3(l.grid), dim3(l.nw * 64), l.lds, st, p.w, p.x, p.gamma, (int)p.chunk, (int)p.ldx, p.K,
@@ -370,6 +383,12 @@ int launch_wide_kernel(const StreamParams& p, const WideLaunch& l, int nblk, hip
 
 template <int WF, int MM>
 int launch_wide_upw(const StreamParams& p, const WideLaunch& l, int nblk, hipStream_t st) {
+    // the int4 decode shapes with the block count fixed at compile time: 2
+    // units per wave over 5 (gate|up N20480) or 2 (qkv N6144) blocks
+    if constexpr (MM <= 2 && tiled_i4(WF)) {
+        if (l.upw == 2 && l.T == 5 && nblk % 5 == 0) return launch_wide_kernel<WF, MM, 2, 5>(p, l, nblk, st);
+        if (l.upw == 2 && l.T == 2 && nblk % 2 == 0) return launch_wide_kernel<WF, MM, 2, 2>(p, l, nblk, st);
+    }
     switch (l.upw) {
         case 2: return launch_wide_kernel<WF, MM, 2>(p, l, nblk, st);
         case 3: return launch_wide_kernel<WF, MM, 3>(p, l, nblk, st);
